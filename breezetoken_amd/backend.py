@@ -1,0 +1,329 @@
+"""Host side of the MI355X GQA attention path, mirroring the reference operator API.
+
+``HipBackend`` exposes the attention part of the reference ``Backend`` protocol
+(breezetoken/backends.py:47-51, 657-706) with the same names, argument meaning
+and shapes, so the Qwen3.5 attention layers call it unchanged:
+
+* ``attention(q, k, v, scale)``: q (H, D), k/v (S, Hkv, D) -> (H, D) f32
+  (eager decode, layers.py:75-80);
+* ``attention_fixed(q, k, v, pos, scale)``: k/v the whole (cap, Hkv, D) cache,
+  ``pos`` a device int32 (1,) holding the 0-based index of the token being
+  decoded, valid length pos + 1 (graph decode, graph.py:55-61).
+
+and adds the operators the reference runs outside the protocol:
+
+* ``attention_prefill(q, k, v, scale)``: causal GQA over a prompt that starts
+  at slot 0, q (S, H, D), k/v (S, Hkv, D) -> (S, H, D) (the SDPA call of
+  prefill.py:56-68); ``sdpa_prefill`` takes that call's (1, H, S, D) layout;
+* ``attention_ragged(...)``: many sequences in one shared cache.
+
+Every launch goes through libbreezetoken_amd.so on torch's current stream with
+no host synchronisation, so the calls can be captured in a hipGraph
+(``torch.cuda.graph``).  There is no torch or CPU fallback: a shape or dtype
+the kernels do not serve raises ``RuntimeError`` (for ``attention_fixed`` this
+is the same signal the reference uses to fall back to eager decode,
+backends.py:698 with graph.py:127-133).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import BT_DTYPE_BF16, BT_DTYPE_F32, check
+
+SERVED_HEAD_DIMS = (64, 128, 256)
+SERVED_PREFILL_HEAD_DIMS = (128, 256)
+MAX_GROUP = 8
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return BT_DTYPE_F32
+    if dt == torch.bfloat16:
+        return BT_DTYPE_BF16
+    raise RuntimeError(f"dtype {dt} is not served (f32 or bf16)")
+
+
+class HipBackend:
+    """MI355X GQA attention backend (decode, fixed-capacity decode, prefill, ragged)."""
+
+    name = "hip"
+
+    def __init__(self, device: str | torch.device = "cuda") -> None:
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError(f"the HIP backend needs a GPU device, got {device!r}")
+        if not torch.cuda.is_available():
+            raise RuntimeError("no ROCm GPU is visible")
+        if dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        self.device = str(dev)
+        self._dev = dev
+        self._family = "cuda"  # torch on ROCm keeps the "cuda" device type
+        self._lib = _lib.lib()
+        props = torch.cuda.get_device_properties(dev)
+        self.num_cus = int(props.multi_processor_count)
+        self.arch = getattr(props, "gcnArchName", "")
+        self._ws: dict[tuple, torch.Tensor] = {}
+        self._plans: dict[tuple, tuple] = {}
+
+    # ------------------------------------------------------------------ utils
+    def _workspace(self, heads: int, dim: int, total_splits: int) -> torch.Tensor:
+        key = (heads, dim, total_splits)
+        ws = self._ws.get(key)
+        if ws is None:
+            nbytes = int(self._lib.bt_decode_workspace_bytes(heads, dim, total_splits))
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=self._dev)
+            self._ws[key] = ws  # kept until close(): captured graphs may point at it
+        return ws
+
+    def pick_splits(self, kv_heads: int, ctx_len: int) -> int:
+        return int(self._lib.bt_decode_pick_splits(kv_heads, ctx_len, self.num_cus))
+
+    def _check_kv(self, k: torch.Tensor, v: torch.Tensor, heads: int, dim: int) -> int:
+        if k.ndim != 3 or v.shape != k.shape:
+            raise RuntimeError("k/v must be (S, Hkv, D) with equal shapes")
+        groups = k.shape[1]
+        if k.shape[2] != dim or heads % groups:
+            raise RuntimeError(f"q heads {heads} / kv {tuple(k.shape)} do not form a GQA group")
+        if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+            raise RuntimeError("the MI355X path serves a bf16 KV cache only")
+        if k.device != self._dev or v.device != self._dev:
+            raise RuntimeError("k/v must live on the backend's device")
+        if k.stride(2) != 1 or k.stride() != v.stride():
+            raise RuntimeError("k/v need unit d-stride and identical strides")
+        if dim not in SERVED_HEAD_DIMS or heads // groups > MAX_GROUP:
+            raise RuntimeError(f"shape H={heads} Hkv={groups} D={dim} is not served")
+        return groups
+
+    # ----------------------------------------------------------- decode (eager)
+    def attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> torch.Tensor:
+        """GQA decode attention; q (H, D), k/v (S, Hkv, D) -> (H, D) f32 (backends.py:47-51)."""
+        if q.ndim != 2 or k.ndim != 3 or v.ndim != 3:
+            raise ValueError("attention expects q (H, D), k/v (S, Hkv, D)")
+        heads, dim = q.shape
+        groups = self._check_kv(k, v, heads, dim)
+        seq = k.shape[0]
+        if seq < 1:
+            raise ValueError("attention needs at least one key")
+        return self._decode(q, k, v, scale, groups, seqlen=seq, pos=None, ctx=seq)
+
+    # ------------------------------------------------------ decode (graph path)
+    def attention_fixed(
+        self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor, scale: float
+    ) -> torch.Tensor:
+        """Fixed-capacity decode for the graph path (backends.py:682-706).
+
+        k/v are the whole ``(cap, Hkv, D)`` cache; keys ``j <= pos[0]`` are valid.
+        Split ranges are derived from ``pos`` on the device, so the launch shape
+        is fixed for a given cache and the call can be captured once and replayed.
+        """
+        if q.ndim != 2 or k.ndim != 3 or v.ndim != 3:
+            raise RuntimeError("fixed attention expects q (H, D), k/v (cap, Hkv, D)")
+        heads, dim = q.shape
+        groups = self._check_kv(k, v, heads, dim)
+        if pos.dtype != torch.int32:
+            pos = pos.reshape(1).to(torch.int32)  # as backends.py:561
+        if pos.device != self._dev:
+            raise RuntimeError("pos must be a device tensor")
+        return self._decode(q, k, v, scale, groups, seqlen=0, pos=pos.reshape(-1)[:1], ctx=k.shape[0])
+
+    def _decode(self, q, k, v, scale, groups, *, seqlen: int, pos, ctx: int) -> torch.Tensor:
+        heads, dim = q.shape
+        if q.dtype not in (torch.float32, torch.bfloat16):
+            raise RuntimeError("q must be f32 or bf16")
+        if q.device != self._dev:
+            raise RuntimeError("q must live on the backend's device")
+        q = q.contiguous()
+        ns = self.pick_splits(groups, ctx)
+        ws = self._workspace(heads, dim, ns)
+        out = torch.empty((heads, dim), dtype=torch.float32, device=self._dev)
+        rc = self._lib.bt_gqa_decode(
+            q.data_ptr(), _dtype_code(q.dtype), heads * dim,
+            k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+            None, _ptr(pos), None, seqlen,
+            1, heads, groups, dim, ns, float(scale),
+            ws.data_ptr(), ws.numel(), out.data_ptr(), BT_DTYPE_F32, heads * dim,
+            _stream(self._dev),
+        )
+        check("bt_gqa_decode", rc)
+        return out
+
+    def decode_partials(
+        self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, num_split: int,
+        pos: torch.Tensor | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """The split pass alone: (lse (H, NS) log2-domain, part (H, NS, D)) (attention.py:88-166)."""
+        heads, dim = q.shape
+        groups = self._check_kv(k, v, heads, dim)
+        q = q.contiguous()
+        lse = torch.empty((heads, num_split), dtype=torch.float32, device=self._dev)
+        part = torch.zeros((heads, num_split, dim), dtype=torch.float32, device=self._dev)
+        rc = self._lib.bt_gqa_decode_split(
+            q.data_ptr(), _dtype_code(q.dtype), heads * dim,
+            k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+            None, _ptr(pos), None, 0 if pos is not None else k.shape[0],
+            1, heads, groups, dim, num_split, float(scale),
+            lse.data_ptr(), part.data_ptr(), _stream(self._dev),
+        )
+        check("bt_gqa_decode_split", rc)
+        return lse, part
+
+    def combine(self, lse: torch.Tensor, part: torch.Tensor) -> torch.Tensor:
+        """The LSE combine alone (attention.py:168-189): (H, NS), (H, NS, D) -> (H, D) f32."""
+        heads, ns, dim = part.shape
+        out = torch.empty((heads, dim), dtype=torch.float32, device=self._dev)
+        rc = self._lib.bt_gqa_decode_combine(
+            lse.contiguous().data_ptr(), part.contiguous().data_ptr(), 1, heads, dim, ns,
+            None, None, ns, out.data_ptr(), BT_DTYPE_F32, heads * dim, _stream(self._dev),
+        )
+        check("bt_gqa_decode_combine", rc)
+        return out
+
+    # ---------------------------------------------------------- batched decode
+    def attention_batched(
+        self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor,
+        seq_offset: torch.Tensor, scale: float, max_len: int,
+    ) -> torch.Tensor:
+        """B sequences sharing one cache, uniform split count; q (B, H, D), pos (B,) int32,
+        seq_offset (B,) int64 first slot of each sequence -> (B, H, D) f32."""
+        batch, heads, dim = q.shape
+        groups = self._check_kv(k, v, heads, dim)
+        q = q.contiguous()
+        ns = max(1, self.pick_splits(groups * batch, max_len))
+        ws = self._workspace(heads, dim, batch * ns)
+        out = torch.empty((batch, heads, dim), dtype=torch.float32, device=self._dev)
+        rc = self._lib.bt_gqa_decode(
+            q.data_ptr(), _dtype_code(q.dtype), heads * dim,
+            k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+            seq_offset.data_ptr(), pos.data_ptr(), None, 0,
+            batch, heads, groups, dim, ns, float(scale),
+            ws.data_ptr(), ws.numel(), out.data_ptr(), BT_DTYPE_F32, heads * dim,
+            _stream(self._dev),
+        )
+        check("bt_gqa_decode", rc)
+        return out
+
+    # ----------------------------------------------------------- ragged decode
+    def ragged_plan(self, lens: list[int], kv_heads: int, target_groups: int | None = None):
+        """Per-sequence split counts proportional to length, as device tables (cached)."""
+        if target_groups is None:
+            target_groups = max(1, self.num_cus // max(1, kv_heads))
+        key = (tuple(int(x) for x in lens), int(target_groups))
+        plan = self._plans.get(key)
+        if plan is not None:
+            return plan
+        batch = len(lens)
+        cap = sum(max(1, -(-int(x) // 32)) for x in lens)
+        lens_c = (ctypes.c_int32 * batch)(*[int(x) for x in lens])
+        work = (ctypes.c_int32 * (4 * cap))()
+        base = (ctypes.c_int32 * batch)()
+        count = (ctypes.c_int32 * batch)()
+        total = ctypes.c_int32()
+        n = self._lib.bt_ragged_plan(
+            ctypes.addressof(lens_c), batch, int(target_groups), ctypes.addressof(work), cap,
+            ctypes.addressof(base), ctypes.addressof(count), ctypes.addressof(total),
+        )
+        if n < 0:
+            check("bt_ragged_plan", n)
+        dev = self._dev
+        work_t = torch.tensor(list(work)[: 4 * n], dtype=torch.int32).to(dev)
+        base_t = torch.tensor(list(base), dtype=torch.int32).to(dev)
+        count_t = torch.tensor(list(count), dtype=torch.int32).to(dev)
+        plan = (work_t, n, base_t, count_t, int(total.value))
+        self._plans[key] = plan
+        return plan
+
+    def attention_ragged(
+        self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_offset: torch.Tensor,
+        seq_len: torch.Tensor, lens: list[int], scale: float, target_groups: int | None = None,
+    ) -> torch.Tensor:
+        """Ragged decode: sequence b reads slots [seq_offset[b], seq_offset[b] + seq_len[b]).
+
+        q (B, H, D); seq_offset (B,) int64 and seq_len (B,) int32 on the device;
+        ``lens`` the same lengths on the host, used only to plan split counts.
+        """
+        batch, heads, dim = q.shape
+        groups = self._check_kv(k, v, heads, dim)
+        if seq_offset.dtype != torch.int64 or seq_len.dtype != torch.int32:
+            raise RuntimeError("seq_offset must be int64 and seq_len int32")
+        q = q.contiguous()
+        work, n, base, count, total = self.ragged_plan(lens, groups, target_groups)
+        ws = self._workspace(heads, dim, total)
+        out = torch.empty((batch, heads, dim), dtype=torch.float32, device=self._dev)
+        rc = self._lib.bt_gqa_decode_ragged(
+            q.data_ptr(), _dtype_code(q.dtype), heads * dim,
+            k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+            seq_offset.data_ptr(), seq_len.data_ptr(), batch, heads, groups, dim,
+            work.data_ptr(), n, base.data_ptr(), count.data_ptr(), total, float(scale),
+            ws.data_ptr(), ws.numel(), out.data_ptr(), BT_DTYPE_F32, heads * dim,
+            _stream(self._dev),
+        )
+        check("bt_gqa_decode_ragged", rc)
+        return out
+
+    # ------------------------------------------------------------------ prefill
+    def attention_prefill(
+        self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+        out_dtype: torch.dtype = torch.float32,
+    ) -> torch.Tensor:
+        """Causal GQA prefill (prefill.py:56-68): q (S, H, D), k/v (S, Hkv, D) bf16 -> (S, H, D)."""
+        if q.ndim != 3 or k.ndim != 3 or v.shape != k.shape:
+            raise ValueError("prefill expects q (S, H, D), k/v (S, Hkv, D)")
+        steps, heads, dim = q.shape
+        groups = k.shape[1]
+        if k.shape[0] != steps or k.shape[2] != dim or heads % groups:
+            raise RuntimeError("prefill q/k/v shapes do not match")
+        if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+            raise RuntimeError("the MFMA prefill serves bf16 q/k/v")
+        if dim not in SERVED_PREFILL_HEAD_DIMS or heads // groups > MAX_GROUP:
+            raise RuntimeError(f"prefill shape H={heads} Hkv={groups} D={dim} is not served")
+        for t in (q, k, v):
+            if t.stride(2) != 1:
+                raise RuntimeError("prefill needs unit d-stride")
+        if k.stride() != v.stride():
+            raise RuntimeError("k and v need identical strides")
+        out = torch.empty((steps, heads, dim), dtype=out_dtype, device=self._dev)
+        rc = self._lib.bt_gqa_prefill(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1),
+            k.stride(0), k.stride(1), steps, heads, groups, dim, float(scale),
+            out.data_ptr(), _dtype_code(out_dtype), out.stride(0), out.stride(1),
+            _stream(self._dev),
+        )
+        check("bt_gqa_prefill", rc)
+        return out
+
+    def sdpa_prefill(
+        self, qq: torch.Tensor, kk: torch.Tensor, vv: torch.Tensor, scale: float,
+        out_dtype: torch.dtype = torch.float32,
+    ) -> torch.Tensor:
+        """Drop-in for prefill.py:60-68: (1, H, S, D), (1, Hkv, S, D) -> (1, H, S, D)."""
+        out = self.attention_prefill(
+            qq[0].transpose(0, 1), kk[0].transpose(0, 1), vv[0].transpose(0, 1), scale, out_dtype
+        )
+        return out.transpose(0, 1).unsqueeze(0)
+
+    def close(self) -> None:
+        self._ws.clear()
+        self._plans.clear()
+
+    def __repr__(self) -> str:
+        return f"HipBackend(device={self.device!r}, arch={self.arch!r}, cus={self.num_cus})"
+
+
+def make_backend(kind: str = "hip", device: str = "cuda") -> HipBackend:
+    """Factory in the spirit of ``make_backend`` (backends.py:860-903) for this path."""
+    if kind not in ("hip", "auto"):
+        raise ValueError(f"unknown backend {kind!r}")
+    return HipBackend(device)

@@ -1,0 +1,83 @@
+// Shared device helpers for the gfx950 GQA attention kernels.
+//
+// Conventions used across the kernels:
+//  * bf16 values travel as raw 16-bit patterns (uint16_t) in memory and are
+//    only reinterpreted as __bf16 vectors when handed to an MFMA.  Whole
+//    vectors are bit-cast; single bf16 lanes are never extracted from a
+//    vector (hipcc 7.2 folds such extracts of ds_read_tr results wrongly).
+//  * MFMA operand layouts (verified on gfx950):
+//      v_mfma_f32_16x16x32_bf16: lane l holds A[l%16][(l/16)*8 + 0..7],
+//        B[(l/16)*8 + 0..7][l%16]; C[(l/16)*4 + j][l%16] in acc[j].
+//      v_mfma_f32_32x32x16_bf16: lane l holds A[l%32][(l/32)*8 + 0..7],
+//        B[(l/32)*8 + 0..7][l%32]; C[(j/4)*8 + (l/32)*4 + j%4][l%32] in acc[j].
+//  * ds_read_b64_tr_b16 (per 16-lane group): input lane i points at row i/4,
+//    columns (i%4)*4 .. +3 of a 4x16 block of 16-bit values; output lane j
+//    receives column j, rows 0..3.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bt {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define BT_LDS __attribute__((address_space(3)))
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <- lane 15-i within each row of 16
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <- lane 7-i within each half-row of 8
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// float -> bf16 bits, round to nearest even (inputs are finite or +-inf).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) {
+  return (lo16 & 0xffffu) | (hi16 << 16);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ floatx4 mfma16(const bf16x8& a, const bf16x8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx16 mfma32(const bf16x8& a, const bf16x8& b, const floatx16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Two transposed 4x16 reads glued into one 8-element MFMA operand.
+__device__ __forceinline__ bf16x8 lds_read_tr_pair(const BT_LDS uint16_t* p0, const BT_LDS uint16_t* p1) {
+  bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((BT_LDS bf16x4*)p0);
+  bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((BT_LDS bf16x4*)p1);
+  u32x2 ua = __builtin_bit_cast(u32x2, a);
+  u32x2 ub = __builtin_bit_cast(u32x2, b);
+  u32x4 r = {ua[0], ua[1], ub[0], ub[1]};
+  return as_bf16x8(r);
+}
+
+__device__ __forceinline__ float wave_max_xor(float x, int mask) {
+  return fmaxf(x, __shfl_xor(x, mask, 64));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+}  // namespace bt

@@ -1,0 +1,67 @@
+// Internal launch interface between the C ABI (capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bt {
+
+// Largest number of splits one sequence may use (LSE weights live in LDS).
+constexpr int kMaxSplitsPerSeq = 4096;
+
+struct DecodeSplitParams {
+  const void* q;             // (batch, heads, D) f32 or bf16; head stride = D
+  int64_t q_stride_seq;      // elements between sequences in q
+  int q_bf16;                // 1: q is bf16, 0: f32
+  const uint16_t* k;         // bf16 cache, token-major
+  const uint16_t* v;
+  int64_t kv_stride_tok;     // elements between consecutive token slots
+  int64_t kv_stride_head;    // elements between kv heads of one slot
+  const int64_t* seq_offset; // (batch,) first slot of each sequence, or null (0)
+  const int32_t* pos;        // (batch,) valid = pos + 1, or null
+  const int32_t* seq_len;    // (batch,) valid lengths, or null
+  int32_t seqlen;            // valid length when pos and seq_len are null
+  const int4* work;          // (num_work,) {b, s, ns_b, base_b}, or null: uniform num_split
+  int32_t num_split;
+  int32_t total_splits;      // row length of lse / part per head
+  int32_t heads;
+  int32_t kv_heads;
+  float scale_log2;          // softmax scale * log2(e)
+  float* lse;                // (heads, total_splits)
+  float* part;               // (heads, total_splits, D)
+};
+
+struct CombineParams {
+  const float* lse;
+  const float* part;
+  int32_t num_split;            // uniform split count (split_base == null)
+  int32_t total_splits;
+  const int32_t* split_base;    // (batch,) first split of each sequence, or null
+  const int32_t* split_count;   // (batch,) splits of each sequence, or null
+  void* out;                    // (batch, heads, D)
+  int out_bf16;
+  int64_t out_stride_seq;
+};
+
+struct PrefillParams {
+  const uint16_t* q;   // bf16 (S, H, D) with strides
+  const uint16_t* k;   // bf16 (S, Hkv, D)
+  const uint16_t* v;
+  int64_t q_stride_tok, q_stride_head;
+  int64_t kv_stride_tok, kv_stride_head;
+  int32_t seqlen;
+  int32_t heads;
+  int32_t kv_heads;
+  float scale_log2;
+  void* out;
+  int out_bf16;
+  int64_t out_stride_tok, out_stride_head;
+};
+
+hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int grid_x, int batch,
+                               hipStream_t stream);
+hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads, int batch,
+                                 hipStream_t stream);
+hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stream);
+
+}  // namespace bt

@@ -1,0 +1,285 @@
+// The C ABI of libbreezetoken_amd.so: argument validation and launches.
+// Declarations and documentation live in include/breezetoken_amd.h.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/breezetoken_amd.h"
+#include "bt_kernels.h"
+
+namespace {
+
+constexpr double kLog2e = 1.4426950408889634;
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool served_dim(int d) { return d == 64 || d == 128 || d == 256; }
+inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+int check_decode_common(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
+                        const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                        int32_t batch, int32_t heads, int32_t kv_heads, int32_t head_dim) {
+  if (!q || !k || !v) return BT_EINVAL;
+  if (batch < 1 || heads < 1 || kv_heads < 1 || head_dim < 1) return BT_EINVAL;
+  if (heads % kv_heads != 0) return BT_EINVAL;
+  if (q_dtype != BT_DTYPE_F32 && q_dtype != BT_DTYPE_BF16) return BT_EINVAL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return BT_EINVAL;
+  if (kv_stride_tok <= 0 || kv_stride_head < 0 || kv_stride_tok % 8 || kv_stride_head % 8)
+    return BT_EINVAL;
+  if (batch > 1 && (q_stride_seq < (int64_t)heads * head_dim || q_stride_seq % 8)) return BT_EINVAL;
+  if (!served_dim(head_dim)) return BT_ENOTSUP;
+  if (heads / kv_heads > 8) return BT_ENOTSUP;
+  if (batch > 65535 || kv_heads > 65535) return BT_ENOTSUP;
+  return BT_OK;
+}
+
+int check_out(const void* out, int32_t out_dtype, int64_t out_stride_seq, int32_t batch,
+              int32_t heads, int32_t head_dim) {
+  if (!out) return BT_EINVAL;
+  if (out_dtype != BT_DTYPE_F32 && out_dtype != BT_DTYPE_BF16) return BT_EINVAL;
+  if (!aligned16(out)) return BT_EINVAL;
+  if (batch > 1 && (out_stride_seq < (int64_t)heads * head_dim || out_stride_seq % 8))
+    return BT_EINVAL;
+  return BT_OK;
+}
+
+bt::DecodeSplitParams make_split_params(const void* q, int32_t q_dtype, int64_t q_stride_seq,
+                                        const void* k, const void* v, int64_t kv_stride_tok,
+                                        int64_t kv_stride_head, const int64_t* seq_offset,
+                                        const int32_t* pos, const int32_t* seq_len,
+                                        int32_t seqlen, int32_t heads, int32_t kv_heads,
+                                        int32_t head_dim, float scale, float* lse, float* part) {
+  bt::DecodeSplitParams p{};
+  p.q = q;
+  p.q_stride_seq = q_stride_seq > 0 ? q_stride_seq : (int64_t)heads * head_dim;
+  p.q_bf16 = q_dtype == BT_DTYPE_BF16;
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.kv_stride_tok = kv_stride_tok;
+  p.kv_stride_head = kv_stride_head;
+  p.seq_offset = seq_offset;
+  p.pos = pos;
+  p.seq_len = seq_len;
+  p.seqlen = seqlen;
+  p.heads = heads;
+  p.kv_heads = kv_heads;
+  p.scale_log2 = (float)((double)scale * kLog2e);
+  p.lse = lse;
+  p.part = part;
+  return p;
+}
+
+inline int hip_rc(hipError_t e) { return e == hipSuccess ? BT_OK : (int)e; }
+
+}  // namespace
+
+extern "C" {
+
+int bt_version(void) { return 100; }
+
+const char* bt_strerror(int code) {
+  switch (code) {
+    case BT_OK: return "success";
+    case BT_EINVAL: return "invalid argument (null pointer, shape, stride or alignment)";
+    case BT_ENOTSUP: return "shape not served (head_dim, group size or split count)";
+    case BT_ENOSPC: return "workspace too small";
+    default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
+  }
+}
+
+int64_t bt_decode_workspace_bytes(int32_t heads, int32_t head_dim, int32_t total_splits) {
+  if (heads < 1 || head_dim < 1 || total_splits < 1) return 0;
+  const int64_t lse = align256((int64_t)heads * total_splits * 4);
+  return lse + (int64_t)heads * total_splits * head_dim * 4;
+}
+
+int32_t bt_decode_pick_splits(int32_t kv_heads, int32_t ctx_len, int32_t num_cus) {
+  if (kv_heads < 1) kv_heads = 1;
+  if (num_cus < 1) num_cus = 256;
+  int32_t ns = (num_cus + kv_heads - 1) / kv_heads;
+  const int32_t tiles = ctx_len > 0 ? (ctx_len + 31) / 32 : 1;
+  if (ns > tiles) ns = tiles;
+  if (ns > bt::kMaxSplitsPerSeq) ns = bt::kMaxSplitsPerSeq;
+  return ns < 1 ? 1 : ns;
+}
+
+int bt_gqa_decode_split(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
+                        const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                        const int64_t* seq_offset, const int32_t* pos, const int32_t* seq_len,
+                        int32_t seqlen, int32_t batch, int32_t heads, int32_t kv_heads,
+                        int32_t head_dim, int32_t num_split, float scale, float* lse,
+                        float* part, void* stream) {
+  int rc = check_decode_common(q, q_dtype, q_stride_seq, k, v, kv_stride_tok, kv_stride_head,
+                               batch, heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!lse || !part || !aligned16(part)) return BT_EINVAL;
+  if (num_split < 1) return BT_EINVAL;
+  if (num_split > bt::kMaxSplitsPerSeq) return BT_ENOTSUP;
+  if (!pos && !seq_len && seqlen < 0) return BT_EINVAL;
+  if ((int64_t)batch * num_split > INT32_MAX / 2) return BT_ENOTSUP;
+  bt::DecodeSplitParams p = make_split_params(q, q_dtype, q_stride_seq, k, v, kv_stride_tok,
+                                              kv_stride_head, seq_offset, pos, seq_len, seqlen,
+                                              heads, kv_heads, head_dim, scale, lse, part);
+  p.work = nullptr;
+  p.num_split = num_split;
+  p.total_splits = batch * num_split;
+  return hip_rc(bt::launch_decode_split(p, head_dim, num_split, batch, (hipStream_t)stream));
+}
+
+int bt_gqa_decode_combine(const float* lse, const float* part, int32_t batch, int32_t heads,
+                          int32_t head_dim, int32_t num_split, const int32_t* split_base,
+                          const int32_t* split_count, int32_t total_splits, void* out,
+                          int32_t out_dtype, int64_t out_stride_seq, void* stream) {
+  if (!lse || !part || !aligned16(part)) return BT_EINVAL;
+  if (batch < 1 || heads < 1 || total_splits < 1) return BT_EINVAL;
+  if ((split_base == nullptr) != (split_count == nullptr)) return BT_EINVAL;
+  if (!split_base && (num_split < 1 || (int64_t)batch * num_split > total_splits)) return BT_EINVAL;
+  if (!split_base && num_split > bt::kMaxSplitsPerSeq) return BT_ENOTSUP;
+  if (!served_dim(head_dim)) return BT_ENOTSUP;
+  if (heads > 65535 || batch > 65535) return BT_ENOTSUP;
+  int rc = check_out(out, out_dtype, out_stride_seq, batch, heads, head_dim);
+  if (rc) return rc;
+  bt::CombineParams c{};
+  c.lse = lse;
+  c.part = part;
+  c.num_split = num_split;
+  c.total_splits = total_splits;
+  c.split_base = split_base;
+  c.split_count = split_count;
+  c.out = out;
+  c.out_bf16 = out_dtype == BT_DTYPE_BF16;
+  c.out_stride_seq = out_stride_seq > 0 ? out_stride_seq : (int64_t)heads * head_dim;
+  return hip_rc(bt::launch_decode_combine(c, head_dim, heads, batch, (hipStream_t)stream));
+}
+
+int bt_gqa_decode(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
+                  const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                  const int64_t* seq_offset, const int32_t* pos, const int32_t* seq_len,
+                  int32_t seqlen, int32_t batch, int32_t heads, int32_t kv_heads,
+                  int32_t head_dim, int32_t num_split, float scale, void* workspace,
+                  int64_t workspace_bytes, void* out, int32_t out_dtype,
+                  int64_t out_stride_seq, void* stream) {
+  int rc = check_decode_common(q, q_dtype, q_stride_seq, k, v, kv_stride_tok, kv_stride_head,
+                               batch, heads, kv_heads, head_dim);
+  if (rc) return rc;
+  rc = check_out(out, out_dtype, out_stride_seq, batch, heads, head_dim);
+  if (rc) return rc;
+  if (num_split < 1) return BT_EINVAL;
+  if (num_split > bt::kMaxSplitsPerSeq) return BT_ENOTSUP;
+  if ((int64_t)batch * num_split > INT32_MAX / 2) return BT_ENOTSUP;
+  if (!workspace || !aligned16(workspace)) return BT_EINVAL;
+  const int32_t total = batch * num_split;
+  if (workspace_bytes < bt_decode_workspace_bytes(heads, head_dim, total)) return BT_ENOSPC;
+  float* lse = static_cast<float*>(workspace);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                         align256((int64_t)heads * total * 4));
+  rc = bt_gqa_decode_split(q, q_dtype, q_stride_seq, k, v, kv_stride_tok, kv_stride_head,
+                           seq_offset, pos, seq_len, seqlen, batch, heads, kv_heads, head_dim,
+                           num_split, scale, lse, part, stream);
+  if (rc) return rc;
+  return bt_gqa_decode_combine(lse, part, batch, heads, head_dim, num_split, nullptr, nullptr,
+                               total, out, out_dtype, out_stride_seq, stream);
+}
+
+int32_t bt_ragged_plan(const int32_t* lens, int32_t batch, int32_t target_groups, int32_t* work,
+                       int32_t work_capacity, int32_t* split_base, int32_t* split_count,
+                       int32_t* total_splits) {
+  if (!lens || !work || !split_base || !split_count || !total_splits) return BT_EINVAL;
+  if (batch < 1 || target_groups < 1) return BT_EINVAL;
+  int64_t sum = 0;
+  for (int32_t b = 0; b < batch; ++b) {
+    if (lens[b] < 0) return BT_EINVAL;
+    sum += lens[b];
+  }
+  int32_t total = 0;
+  for (int32_t b = 0; b < batch; ++b) {
+    const int32_t tiles = (lens[b] + 31) / 32;
+    int64_t ns = sum > 0 ? ((int64_t)target_groups * lens[b] + sum - 1) / sum : 1;
+    if (ns > tiles) ns = tiles;
+    if (ns > bt::kMaxSplitsPerSeq) ns = bt::kMaxSplitsPerSeq;
+    if (ns < 1) ns = 1;
+    split_base[b] = total;
+    split_count[b] = (int32_t)ns;
+    if ((int64_t)total + ns > work_capacity) return BT_ENOSPC;
+    for (int32_t s = 0; s < ns; ++s) {
+      int32_t* w = work + 4 * (int64_t)(total + s);
+      w[0] = b;
+      w[1] = s;
+      w[2] = (int32_t)ns;
+      w[3] = total;
+    }
+    total += (int32_t)ns;
+  }
+  *total_splits = total;
+  return total;
+}
+
+int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
+                         const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                         const int64_t* seq_offset, const int32_t* seq_len, int32_t batch,
+                         int32_t heads, int32_t kv_heads, int32_t head_dim, const int32_t* work,
+                         int32_t num_work, const int32_t* split_base, const int32_t* split_count,
+                         int32_t total_splits, float scale, void* workspace,
+                         int64_t workspace_bytes, void* out, int32_t out_dtype,
+                         int64_t out_stride_seq, void* stream) {
+  int rc = check_decode_common(q, q_dtype, q_stride_seq, k, v, kv_stride_tok, kv_stride_head,
+                               batch, heads, kv_heads, head_dim);
+  if (rc) return rc;
+  rc = check_out(out, out_dtype, out_stride_seq, batch, heads, head_dim);
+  if (rc) return rc;
+  if (!seq_offset || !seq_len || !work || !split_base || !split_count) return BT_EINVAL;
+  if (num_work < 1 || total_splits < num_work) return BT_EINVAL;
+  if (!workspace || !aligned16(workspace)) return BT_EINVAL;
+  if (workspace_bytes < bt_decode_workspace_bytes(heads, head_dim, total_splits)) return BT_ENOSPC;
+  if (!aligned16(work)) return BT_EINVAL;
+  float* lse = static_cast<float*>(workspace);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                         align256((int64_t)heads * total_splits * 4));
+  bt::DecodeSplitParams p = make_split_params(q, q_dtype, q_stride_seq, k, v, kv_stride_tok,
+                                              kv_stride_head, seq_offset, nullptr, seq_len, 0,
+                                              heads, kv_heads, head_dim, scale, lse, part);
+  p.work = reinterpret_cast<const int4*>(work);
+  p.num_split = 0;
+  p.total_splits = total_splits;
+  rc = hip_rc(bt::launch_decode_split(p, head_dim, num_work, 1, (hipStream_t)stream));
+  if (rc) return rc;
+  return bt_gqa_decode_combine(lse, part, batch, heads, head_dim, 0, split_base, split_count,
+                               total_splits, out, out_dtype, out_stride_seq, stream);
+}
+
+int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
+                   int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
+                   int32_t seqlen, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
+                   void* out, int32_t out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
+                   void* stream) {
+  if (!q || !k || !v || !out) return BT_EINVAL;
+  if (seqlen < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads) return BT_EINVAL;
+  if (out_dtype != BT_DTYPE_F32 && out_dtype != BT_DTYPE_BF16) return BT_EINVAL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return BT_EINVAL;
+  if (q_stride_tok <= 0 || q_stride_head <= 0 || kv_stride_tok <= 0 || kv_stride_head < 0 ||
+      out_stride_tok <= 0 || out_stride_head <= 0)
+    return BT_EINVAL;
+  if (q_stride_tok % 8 || q_stride_head % 8 || kv_stride_tok % 8 || kv_stride_head % 8 ||
+      out_stride_tok % 8 || out_stride_head % 8)
+    return BT_EINVAL;
+  if (head_dim != 256 && head_dim != 128) return BT_ENOTSUP;
+  if (heads / kv_heads > 8) return BT_ENOTSUP;
+  bt::PrefillParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.q_stride_tok = q_stride_tok;
+  p.q_stride_head = q_stride_head;
+  p.kv_stride_tok = kv_stride_tok;
+  p.kv_stride_head = kv_stride_head;
+  p.seqlen = seqlen;
+  p.heads = heads;
+  p.kv_heads = kv_heads;
+  p.scale_log2 = (float)((double)scale * kLog2e);
+  p.out = out;
+  p.out_bf16 = out_dtype == BT_DTYPE_BF16;
+  p.out_stride_tok = out_stride_tok;
+  p.out_stride_head = out_stride_head;
+  return hip_rc(bt::launch_prefill(p, head_dim, (hipStream_t)stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,131 @@
+/*
+ * breezetoken_amd -- MI355X (gfx950) GQA attention behind a plain C ABI.
+ *
+ * Every entry point takes device pointers, element strides and a hipStream_t
+ * (passed as void*), launches asynchronously on that stream, never allocates,
+ * never synchronises and never reads device memory from the host, so every
+ * call can be captured in a hipGraph.  Return value: BT_OK (0), a negative
+ * BT_E* code for an argument the library refuses (nothing is launched), or a
+ * positive hipError_t if the launch itself failed.
+ *
+ * Layouts:
+ *   q       (batch, heads, head_dim)          f32 or bf16, head stride = head_dim
+ *   k, v    token-major bf16 cache: element (slot, kv_head, d) at
+ *           slot*kv_stride_tok + kv_head*kv_stride_head + d
+ *           (the reference cache is (max_context, n_kv*head_dim), i.e.
+ *           kv_stride_tok = n_kv*head_dim, kv_stride_head = head_dim)
+ *   lse     (heads, total_splits) f32, log2 domain
+ *   part    (heads, total_splits, head_dim) f32, normalised split outputs
+ *   out     (batch, heads, head_dim) f32 or bf16, sequence stride out_stride_seq
+ *
+ * Query head h reads kv head h / (heads / kv_heads).  Served shapes:
+ * head_dim in {64, 128, 256}, heads / kv_heads in 1..8 (decode) and 1..8
+ * (prefill); pointers 16-byte aligned, strides multiples of 8 elements.
+ */
+#ifndef BREEZETOKEN_AMD_H
+#define BREEZETOKEN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BT_OK 0
+#define BT_EINVAL (-22)  /* malformed argument: null pointer, bad shape, stride or alignment */
+#define BT_ENOTSUP (-95) /* well-formed but not served (head_dim, group size, split count) */
+#define BT_ENOSPC (-28)  /* workspace too small */
+
+#define BT_DTYPE_F32 0
+#define BT_DTYPE_BF16 1
+
+/* Library version: major*10000 + minor*100 + patch. */
+int bt_version(void);
+
+/* Human-readable text for a return code of this library. */
+const char* bt_strerror(int code);
+
+/* Bytes of split workspace (lse + partials) for `total_splits` splits of
+ * `heads` query heads.  Replaces the per-call torch.empty of Lse/Part in
+ * _build_attention / _build_attention_fixed (breezetoken/backends.py:531-533,
+ * 554-556); the caller owns it and may reuse it across calls and graph replays. */
+int64_t bt_decode_workspace_bytes(int32_t heads, int32_t head_dim, int32_t total_splits);
+
+/* Split count for one sequence of up to `ctx_len` tokens on a GPU with
+ * `num_cus` compute units (the reference hard-codes 16, backends.py:526,550). */
+int32_t bt_decode_pick_splits(int32_t kv_heads, int32_t ctx_len, int32_t num_cus);
+
+/* Split-KV pass: the first kernel of gqa_decode / gqa_decode_fixed
+ * (breezetoken/kernels/cuda/attention.py:88-166 and 249-326).  The valid length
+ * of sequence b is pos[b] + 1 when pos != NULL (the device position tensor of
+ * the graph path, attention.py:296-301), else seq_len[b] when seq_len != NULL,
+ * else `seqlen`.  seq_offset (nullable) gives each sequence's first slot.
+ * Writes lse/part rows [b*num_split, (b+1)*num_split) of every head;
+ * total_splits = batch*num_split. */
+int bt_gqa_decode_split(const void* q, int32_t q_dtype, int64_t q_stride_seq,
+                        const void* k, const void* v, int64_t kv_stride_tok,
+                        int64_t kv_stride_head, const int64_t* seq_offset, const int32_t* pos,
+                        const int32_t* seq_len, int32_t seqlen, int32_t batch, int32_t heads,
+                        int32_t kv_heads, int32_t head_dim, int32_t num_split, float scale,
+                        float* lse, float* part, void* stream);
+
+/* LSE combine: the second kernel of gqa_decode (attention.py:168-189, 328-349).
+ * split_base/split_count (device, nullable) select each sequence's splits for
+ * ragged batches; when NULL every sequence owns num_split consecutive splits. */
+int bt_gqa_decode_combine(const float* lse, const float* part, int32_t batch, int32_t heads,
+                          int32_t head_dim, int32_t num_split, const int32_t* split_base,
+                          const int32_t* split_count, int32_t total_splits, void* out,
+                          int32_t out_dtype, int64_t out_stride_seq, void* stream);
+
+/* Split + combine in one call: the launch behind Backend.attention and
+ * attention_fixed (breezetoken/backends.py:523-568, 657-706).  `workspace` must
+ * hold bt_decode_workspace_bytes(heads, head_dim, batch*num_split) bytes. */
+int bt_gqa_decode(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
+                  const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                  const int64_t* seq_offset, const int32_t* pos, const int32_t* seq_len,
+                  int32_t seqlen, int32_t batch, int32_t heads, int32_t kv_heads,
+                  int32_t head_dim, int32_t num_split, float scale, void* workspace,
+                  int64_t workspace_bytes, void* out, int32_t out_dtype,
+                  int64_t out_stride_seq, void* stream);
+
+/* Host-side planner for ragged batches (no device access): given host lengths
+ * lens[batch], choose per-sequence split counts proportional to length so that
+ * about `target_groups` work-groups per kv head exist, and fill
+ *   work[4*i .. 4*i+3] = {b, s, ns_b, base_b} for every split i (capacity
+ *   work_capacity entries), split_base[b], split_count[b], *total_splits.
+ * Returns the number of work entries, or a negative BT_E* code. */
+int32_t bt_ragged_plan(const int32_t* lens, int32_t batch, int32_t target_groups,
+                       int32_t* work, int32_t work_capacity, int32_t* split_base,
+                       int32_t* split_count, int32_t* total_splits);
+
+/* Ragged multi-sequence decode over one shared cache: sequence b occupies
+ * slots [seq_offset[b], seq_offset[b] + seq_len[b]).  `work`, split_base and
+ * split_count are the device copies of bt_ragged_plan's output.  No reference
+ * counterpart (the reference decodes one sequence); it generalises
+ * gqa_decode's split/combine (attention.py:54-205) to a per-sequence table. */
+int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
+                         const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                         const int64_t* seq_offset, const int32_t* seq_len, int32_t batch,
+                         int32_t heads, int32_t kv_heads, int32_t head_dim,
+                         const int32_t* work, int32_t num_work, const int32_t* split_base,
+                         const int32_t* split_count, int32_t total_splits, float scale,
+                         void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
+                         int64_t out_stride_seq, void* stream);
+
+/* Causal GQA prefill attention on bf16 MFMA: replaces the
+ * F.scaled_dot_product_attention(is_causal=True, enable_gqa=True) call of
+ * _prefill_attn (breezetoken/model/prefill.py:56-68).  q (S, heads, D),
+ * k/v (S, kv_heads, D) bf16 with the given strides; query i attends keys 0..i
+ * (the prompt starts at slot 0, prefill.py:54-55).  out (S, heads, D) f32 or
+ * bf16. */
+int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
+                   int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
+                   int32_t seqlen, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                   float scale, void* out, int32_t out_dtype, int64_t out_stride_tok,
+                   int64_t out_stride_head, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BREEZETOKEN_AMD_H */

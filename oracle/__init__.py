@@ -1,0 +1,30 @@
+"""CPU oracle for the GQA attention hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this package, and only as the checker (or, for the CPU
+baseline, as the reference CPU path that is timed beside the GPU).  The product
+path (``breezetoken_amd``) never imports it and has no CPU fallback.
+
+What each function restates, and what pins it (see ``tests/test_oracle.py``):
+
+* ``torch_attention`` / ``torch_attention_einsum`` -- the reference's torch f32
+  decode oracle ``_torch_attention`` (breezetoken/backends.py:196-215), SDPA
+  branch and einsum fallback branch.  Pinned by: agreement of the two branches,
+  f64 brute force, closed forms (S=1, equal keys, dominant key, constant V),
+  permutation invariance, the committed config-1 golden vector.
+* ``torch_prefill_attention`` / ``torch_prefill_einsum`` -- the causal GQA SDPA
+  call of ``_prefill_attn`` (breezetoken/model/prefill.py:56-78) and its
+  einsum+tril fallback.  Pinned by: branch agreement, f64 brute force, row i ==
+  decode over keys 0..i, row 0 == V[0].
+* ``split_partition`` / ``split_decode`` / ``combine_lse`` -- the split-KV
+  partition, per-split log2-domain LSE + normalised partial, empty-split rule
+  and LSE combine of ``gqa_decode`` (breezetoken/kernels/cuda/attention.py:
+  104-112, 153-166, 168-189).  Pinned by: combine(split) == unsplit for every
+  split count, empty split -> (-inf, 0), closed-form LSE.
+* ``fixed_decode`` -- the fixed-capacity/device-position contract of
+  ``gqa_decode_fixed`` (attention.py:296-301, valid = pos + 1) on top of
+  ``torch_attention``.  Pinned by: equality with ``torch_attention`` on the
+  prefix, invariance to garbage written past ``pos``.
+* ``brute_force_decode_f64`` / ``brute_force_prefill_f64`` -- float64 numpy
+  restatements of the attention definition, checked against closed forms.
+"""

@@ -1,0 +1,143 @@
+"""The C ABI library: it loads, exports every declared entry point, and its
+host-only functions (no device work) behave.  No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from breezetoken_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "breezetoken_amd.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(bt_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_python_binding_set():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    assert _lib.LIB_PATH.is_file(), "build with `python -m breezetoken_amd.build`"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (bt_\w+)", out))
+    missing = set(declared_symbols()) - exported
+    assert not missing, missing
+    lib = _lib.lib()
+    for name in declared_symbols():
+        assert getattr(lib, name) is not None
+
+
+def test_library_holds_gfx950_code():
+    out = subprocess.run(["strings", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    assert "gfx950" in out
+
+
+def test_version_and_strerror():
+    lib = _lib.lib()
+    assert lib.bt_version() >= 100
+    assert b"invalid" in lib.bt_strerror(_lib.BT_EINVAL)
+    assert b"not served" in lib.bt_strerror(_lib.BT_ENOTSUP)
+    assert b"workspace" in lib.bt_strerror(_lib.BT_ENOSPC)
+
+
+def test_workspace_bytes():
+    lib = _lib.lib()
+    # lse (8 x 128 f32, padded to 256 B) + part (8 x 128 x 256 f32)
+    assert lib.bt_decode_workspace_bytes(8, 256, 128) == 4096 + 8 * 128 * 256 * 4
+    assert lib.bt_decode_workspace_bytes(8, 256, 1) == 256 + 8 * 256 * 4
+    assert lib.bt_decode_workspace_bytes(0, 256, 1) == 0
+
+
+@pytest.mark.parametrize(
+    "kv,ctx,cus,expect",
+    [(2, 65536, 256, 128), (2, 1024, 256, 32), (2, 1, 256, 1), (1, 32768, 256, 256), (2, 32768, 304, 152)],
+)
+def test_pick_splits(kv, ctx, cus, expect):
+    assert _lib.lib().bt_decode_pick_splits(kv, ctx, cus) == expect
+
+
+def _plan(lens, target):
+    lib = _lib.lib()
+    b = len(lens)
+    cap = sum(max(1, -(-n // 32)) for n in lens)
+    L = (ctypes.c_int32 * b)(*lens)
+    work = (ctypes.c_int32 * (4 * cap))()
+    base = (ctypes.c_int32 * b)()
+    cnt = (ctypes.c_int32 * b)()
+    tot = ctypes.c_int32()
+    n = lib.bt_ragged_plan(ctypes.addressof(L), b, target, ctypes.addressof(work), cap,
+                           ctypes.addressof(base), ctypes.addressof(cnt), ctypes.addressof(tot))
+    return n, list(work)[: 4 * max(n, 0)], list(base), list(cnt), tot.value
+
+
+def test_ragged_plan_is_proportional_and_consistent():
+    lens = [2591, 8912, 338, 24869, 0, 31, 32768]
+    n, work, base, cnt, tot = _plan(lens, 128)
+    assert n == tot == sum(cnt)
+    for b, L in enumerate(lens):
+        assert 1 <= cnt[b] <= max(1, -(-L // 32))
+        assert base[b] == sum(cnt[:b])
+    assert cnt[6] > cnt[3] > cnt[1] > cnt[0] > cnt[2]
+    entries = [tuple(work[4 * i : 4 * i + 4]) for i in range(n)]
+    for i, (b, s, ns, bs) in enumerate(entries):
+        assert ns == cnt[b] and bs == base[b] and bs + s == i
+
+
+def test_ragged_plan_rejects_bad_input():
+    lib = _lib.lib()
+    assert lib.bt_ragged_plan(None, 1, 1, None, 0, None, None, None) == _lib.BT_EINVAL
+    n, *_ = _plan([-1], 4)
+    assert n == _lib.BT_EINVAL
+
+
+def test_entry_points_refuse_bad_arguments_before_launching():
+    """Validation happens on the host; these calls never reach the GPU."""
+    lib = _lib.lib()
+    fake = 1 << 20  # aligned, never dereferenced
+    # null q
+    rc = lib.bt_gqa_decode(None, 0, 0, fake, fake, 512, 256, None, None, None, 16, 1, 8, 2, 256,
+                           16, 0.0625, fake, 1 << 30, fake, 0, 0, None)
+    assert rc == _lib.BT_EINVAL
+    # heads not a multiple of kv_heads
+    rc = lib.bt_gqa_decode(fake, 0, 0, fake, fake, 512, 256, None, None, None, 16, 1, 7, 2, 256,
+                           16, 0.0625, fake, 1 << 30, fake, 0, 0, None)
+    assert rc == _lib.BT_EINVAL
+    # unserved head_dim and group size
+    rc = lib.bt_gqa_decode(fake, 0, 0, fake, fake, 512, 256, None, None, None, 16, 1, 8, 2, 96,
+                           16, 0.0625, fake, 1 << 30, fake, 0, 0, None)
+    assert rc == _lib.BT_ENOTSUP
+    rc = lib.bt_gqa_decode(fake, 0, 0, fake, fake, 512, 256, None, None, None, 16, 1, 32, 2, 256,
+                           16, 0.0625, fake, 1 << 30, fake, 0, 0, None)
+    assert rc == _lib.BT_ENOTSUP
+    # misaligned k, odd stride
+    rc = lib.bt_gqa_decode(fake, 0, 0, fake + 2, fake, 512, 256, None, None, None, 16, 1, 8, 2, 256,
+                           16, 0.0625, fake, 1 << 30, fake, 0, 0, None)
+    assert rc == _lib.BT_EINVAL
+    rc = lib.bt_gqa_decode(fake, 0, 0, fake, fake, 511, 256, None, None, None, 16, 1, 8, 2, 256,
+                           16, 0.0625, fake, 1 << 30, fake, 0, 0, None)
+    assert rc == _lib.BT_EINVAL
+    # workspace too small
+    rc = lib.bt_gqa_decode(fake, 0, 0, fake, fake, 512, 256, None, None, None, 16, 1, 8, 2, 256,
+                           16, 0.0625, fake, 100, fake, 0, 0, None)
+    assert rc == _lib.BT_ENOSPC
+    # too many splits
+    rc = lib.bt_gqa_decode_split(fake, 0, 0, fake, fake, 512, 256, None, None, None, 16, 1, 8, 2,
+                                 256, 5000, 0.0625, fake, fake, None)
+    assert rc == _lib.BT_ENOTSUP
+    # prefill: unserved head dim, bad strides
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 8, 2, 64, 0.125, fake, 0,
+                            2048, 256, None)
+    assert rc == _lib.BT_ENOTSUP
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 0, 8, 2, 256, 0.0625, fake, 0,
+                            2048, 256, None)
+    assert rc == _lib.BT_EINVAL

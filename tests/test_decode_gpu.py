@@ -1,0 +1,212 @@
+"""GPU parity of the split-KV decode kernels against the CPU oracle.
+
+Gate: max-abs error <= 2e-3 and cosine similarity
+>= 0.99999 against the torch f32 reference attention on the same bf16-rounded
+inputs.  Every call goes through libbreezetoken_amd.so.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from breezetoken_amd import workloads as wl
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+COS = 0.99999
+FIXTURE = Path(__file__).resolve().parent / "golden" / "c1_decode.npz"
+
+
+def assert_close(got: torch.Tensor, ref, atol: float = ATOL, cos_min: float = COS) -> None:
+    g = got.detach().float().cpu().numpy()
+    r = ref.detach().float().cpu().numpy() if isinstance(ref, torch.Tensor) else np.asarray(ref)
+    assert np.isfinite(g).all(), "non-finite output"
+    err, cos = orc.compare(g, r)
+    assert err <= atol and cos >= cos_min, f"max-abs {err:.3e}, cosine {cos:.8f}"
+
+
+def _dev(*ts):
+    return [t.to("cuda") for t in ts]
+
+
+def test_c1_golden_vector(hip_backend):
+    with np.load(FIXTURE, allow_pickle=False) as z:
+        g = {k: z[k] for k in z.files}
+
+    def bf(a):
+        return torch.from_numpy(a.astype(np.uint16).view(np.int16).copy()).view(torch.bfloat16)
+
+    q, k, v = bf(g["q_bf16"]), bf(g["k_bf16"]), bf(g["v_bf16"])
+    qd, kd, vd = _dev(q.float(), k, v)
+    out = hip_backend.attention(qd, kd, vd, float(g["scale"]))
+    assert out.shape == (8, 256) and out.dtype == torch.float32
+    assert_close(out, g["out_f32"])
+    assert_close(out, g["out_f64"])
+
+
+@pytest.mark.parametrize("seq", [1, 17, 128])
+def test_reference_kernel_test_shapes(hip_backend, seq):
+    """The shapes of the reference's only attention kernel test (tests/test_cuda.py:194-211),
+    with the cache stored bf16: seed 6, H=8, Hkv=2, D=256."""
+    torch.manual_seed(6)
+    q = torch.randn(8, 256)
+    k = torch.randn(seq, 2, 256).to(torch.bfloat16)
+    v = torch.randn(seq, 2, 256).to(torch.bfloat16)
+    ref = orc.torch_attention(q, k.float(), v.float(), 256**-0.5)
+    out = hip_backend.attention(*_dev(q, k, v), 256**-0.5)
+    assert_close(out, ref)
+
+
+@pytest.mark.parametrize("valid", [1024, 4096, 32768])
+@pytest.mark.parametrize("q_dtype", [torch.float32, torch.bfloat16])
+def test_c2_fixed_capacity_decode(hip_backend, valid, q_dtype):
+    case = wl.c2_inputs(valid)
+    print(f"[c2] valid={valid} q={q_dtype}", flush=True)
+    ref = orc.fixed_decode(case.q.float(), case.k.float(), case.v.float(), case.pos, case.scale)
+    q, k, v = _dev(case.q.to(q_dtype), case.k, case.v)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device="cuda")
+    out = hip_backend.attention_fixed(q, k, v, pos, case.scale)
+    assert_close(out, ref)
+    # the eager path over the valid prefix gives the same answer
+    out2 = hip_backend.attention(q, k[:valid], v[:valid], case.scale)
+    assert_close(out2, ref)
+
+
+@pytest.mark.parametrize("valid", [8192, 32768, 131072])
+def test_c3_outlier_rows(hip_backend, valid):
+    case = wl.c3_inputs(valid)
+    print(f"[c3] valid={valid}", flush=True)
+    ref = orc.torch_attention(case.q.float(), case.k.float(), case.v.float(), case.scale)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device="cuda")
+    assert_close(hip_backend.attention_fixed(q, k, v, pos, case.scale), ref)
+
+
+@pytest.mark.parametrize("valid", [1, 2, 31, 32, 33, 63, 64, 65, 127, 4095, 4096, 4097, 8191, 8192])
+def test_positions_at_tile_and_split_boundaries(hip_backend, valid):
+    case = wl.decode_inputs(21, 8, 2, 256, 8192, valid)
+    ref = orc.fixed_decode(case.q.float(), case.k.float(), case.v.float(), case.pos, case.scale)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device="cuda")
+    assert_close(hip_backend.attention_fixed(q, k, v, pos, case.scale), ref)
+
+
+def test_slots_past_pos_have_no_effect(hip_backend):
+    case = wl.decode_inputs(22, 8, 2, 256, 4096, 1000)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device="cuda")
+    a = hip_backend.attention_fixed(q, k, v, pos, case.scale).clone()
+    k[1000:] = float("nan")
+    v[1000:] = float("inf")
+    b = hip_backend.attention_fixed(q, k, v, pos, case.scale)
+    assert torch.equal(a, b)
+
+
+def test_deterministic(hip_backend):
+    case = wl.c2_inputs(4096, cap=8192)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device="cuda")
+    a = hip_backend.attention_fixed(q, k, v, pos, case.scale).clone()
+    b = hip_backend.attention_fixed(q, k, v, pos, case.scale)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("seq,ns", [(1000, 1), (1000, 3), (1000, 16), (1000, 40), (100, 16), (4096, 128)])
+def test_split_partials_match_oracle(hip_backend, seq, ns):
+    """Per-split LSE (log2 domain) and normalised partials against the restated split
+    kernel (attention.py:114-166); empty splits report lse = -inf."""
+    case = wl.decode_inputs(23, 8, 2, 256, seq, seq)
+    lse_ref, part_ref = orc.split_decode(case.q.float().numpy(), case.k.float().numpy(),
+                                         case.v.float().numpy(), case.scale, ns)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    lse, part = hip_backend.decode_partials(q, k, v, case.scale, ns)
+    lse, part = lse.cpu().numpy(), part.cpu().numpy()
+    empty = np.isneginf(lse_ref)
+    assert np.array_equal(np.isneginf(lse), empty)
+    assert np.abs(lse[~empty] - lse_ref[~empty]).max() < 1e-3
+    full = ~empty
+    assert np.abs(part[full] - part_ref[full]).max() < ATOL
+    # the device combine of device partials equals the oracle combine
+    out = hip_backend.combine(torch.from_numpy(lse).cuda(), torch.from_numpy(part).cuda())
+    assert_close(out, orc.combine_lse(lse_ref, part_ref))
+
+
+def test_combine_of_oracle_partials(hip_backend):
+    case = wl.decode_inputs(24, 8, 2, 256, 2000, 2000)
+    lse, part = orc.split_decode(case.q.float().numpy(), case.k.float().numpy(),
+                                 case.v.float().numpy(), case.scale, 37)
+    out = hip_backend.combine(torch.from_numpy(lse.astype(np.float32)).cuda(),
+                              torch.from_numpy(part.astype(np.float32)).cuda())
+    assert_close(out, orc.combine_lse(lse, part), atol=1e-5)
+
+
+@pytest.mark.parametrize("heads,kv,dim", [(8, 2, 128), (8, 2, 64), (4, 4, 256), (8, 1, 256),
+                                          (16, 2, 128), (6, 2, 256), (12, 2, 64), (2, 1, 256)])
+def test_other_served_shapes(hip_backend, heads, kv, dim):
+    case = wl.decode_inputs(25, heads, kv, dim, 3000, 2345)
+    ref = orc.fixed_decode(case.q.float(), case.k.float(), case.v.float(), case.pos, case.scale)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device="cuda")
+    assert_close(hip_backend.attention_fixed(q, k, v, pos, case.scale), ref)
+
+
+def test_batched_decode_shared_cache(hip_backend):
+    lens = [1, 700, 4096, 2500]
+    offs = [0, 32, 1024, 6144]
+    g = torch.Generator().manual_seed(26)
+    q = torch.randn(4, 8, 256, generator=g).to(torch.bfloat16).float()
+    k = torch.randn(9000, 2, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(9000, 2, 256, generator=g).to(torch.bfloat16)
+    out = hip_backend.attention_batched(
+        q.cuda(), k.cuda(), v.cuda(),
+        torch.tensor([n - 1 for n in lens], dtype=torch.int32, device="cuda"),
+        torch.tensor(offs, dtype=torch.int64, device="cuda"), 256**-0.5, max(lens),
+    )
+    for b, (n, o) in enumerate(zip(lens, offs)):
+        ref = orc.torch_attention(q[b], k[o : o + n].float(), v[o : o + n].float(), 256**-0.5)
+        assert_close(out[b], ref)
+
+
+def test_hipgraph_capture_and_replay(hip_backend):
+    """The fixed-capacity call captured once (torch.cuda.graph = hipGraph on ROCm) with the
+    position advanced on the device inside the graph, as graph.py:83-84 does; every
+    replay is checked against the oracle at its position, with eager work between replays."""
+    case = wl.c2_inputs(2000, cap=4096)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    pos = torch.tensor([1500], dtype=torch.int32, device="cuda")
+    hip_backend.attention_fixed(q, k, v, pos, case.scale)  # preflight outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = hip_backend.attention_fixed(q, k, v, pos, case.scale)
+        pos.add_(1)
+    for step in range(6):
+        p = 1500 + step
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = orc.fixed_decode(case.q.float(), case.k.float(), case.v.float(), p, case.scale)
+        assert_close(got, ref)
+        eager = hip_backend.attention_fixed(q, k, v, torch.tensor([p], dtype=torch.int32, device="cuda"),
+                                            case.scale)
+        assert torch.equal(eager, got)
+    assert int(pos.item()) == 1506
+
+
+def test_unserved_shapes_raise(hip_backend):
+    q = torch.randn(32, 256, device="cuda")
+    k = torch.zeros(64, 2, 256, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(RuntimeError):
+        hip_backend.attention_fixed(q, k, k, torch.zeros(1, dtype=torch.int32, device="cuda"), 0.0625)
+    with pytest.raises(RuntimeError):
+        hip_backend.attention(q[:8], k.float(), k.float(), 0.0625)
+    with pytest.raises(RuntimeError):
+        hip_backend.attention(torch.randn(8, 96, device="cuda"),
+                              torch.zeros(4, 2, 96, dtype=torch.bfloat16, device="cuda"),
+                              torch.zeros(4, 2, 96, dtype=torch.bfloat16, device="cuda"), 0.1)
