@@ -4,13 +4,19 @@
 Headline (BASELINE.json ``metric``, config 2): split-KV GQA flash-decode,
 Qwen3.5-0.8B-like H=8 / Hkv=2 / D=256, bf16 fixed-capacity cache of 65,536
 slots, valid length 32,768 given by a device position tensor, q/K/V ~ N(0, 1)
-bf16 (seed 1).  One step = one decode call (split + LSE combine) captured in a
-hipGraph (``torch.cuda.graph``) and replayed; inputs are resident in HBM.
-``value`` = algorithmic bytes of a call / time per call, in GB/s.
+bf16 (seed 1).  One step = one decode call (split + LSE combine).  The calls
+are captured in a hipGraph (``torch.cuda.graph``) the way the model's decode
+step holds them: one graph per decode step with one call per attention layer
+(the 0.8B model has 6), each on its own layer cache, so a replay streams 6
+distinct 64 MiB prefixes (384 MiB, more than the 256 MB Infinity Cache) from
+HBM.  ``ms_per_step`` = replay time / 6; ``value`` = algorithmic bytes of a
+call / ``ms_per_step``, in GB/s.  A graph holding a single call replayed
+``--steps`` times is reported as ``extra.single_call_graph``.
 
-Also reported (``extra``): 1k/4k/32k decode, config 3, config 5 (ragged), a
-cold-cache variant of config 2 (5 rotating caches > the 256 MB Infinity Cache)
-and causal prefill TFLOP/s (config 4) when the prefill kernel is served.
+Also reported (``extra``): 1k/4k/32k decode, config 3, config 5 (ragged), all
+timed the same way (one call per distinct layer cache inside one graph), a
+MALL-hot variant of config 2 (one cache, 6 calls per graph) for contrast, and
+causal prefill TFLOP/s (config 4) when the prefill kernel is served.
 
 ``roofline`` times the split kernel alone (the dominant kernel) with HIP events
 on the stream it is launched on; ``cpu_baseline`` times the CPU torch f32
@@ -65,6 +71,46 @@ def time_graph(torch, fn, steps: int, warmup: int, calls_per_graph: int = 1) -> 
     return start.elapsed_time(end) / (replays * calls_per_graph)
 
 
+def pmc_mode(torch, backend, dev) -> int:
+    """Launches for counter collection: a plain copy of known size (to scale
+    FETCH_SIZE / WRITE_SIZE) and the config-2 split kernel on 6 layer caches."""
+    import ctypes
+
+    from breezetoken_amd import _lib
+    from breezetoken_amd import workloads as wl
+    from breezetoken_amd.kvcache import KVCache
+
+    H, HKV, D, CAP, L = 8, 2, 256, 65536, 32768
+    src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)  # 256 MiB read + 256 MiB written per launch
+    case = wl.c2_inputs(L, cap=CAP)
+    ns = backend.pick_splits(HKV, CAP)
+    lse = torch.empty((H, ns), dtype=torch.float32, device=dev)
+    part = torch.empty((H, ns, D), dtype=torch.float32, device=dev)
+    q = case.q.float().to(dev)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device=dev)
+    caches = []
+    for _ in range(6):
+        c = KVCache(CAP, HKV, D, dev)
+        c.k.copy_(case.k.reshape(CAP, -1))
+        c.v.copy_(case.v.reshape(CAP, -1))
+        caches.append(c.views() + (c,))
+    lib = _lib.lib()
+    for _ in range(5):
+        for kv, vv, _c in caches:
+            rc = lib.bt_gqa_decode_split(
+                q.data_ptr(), _lib.BT_DTYPE_F32, H * D, kv.data_ptr(), vv.data_ptr(), kv.stride(0),
+                kv.stride(1), None, pos.data_ptr(), None, CAP, 1, H, HKV, D, ns, case.scale,
+                lse.data_ptr(), part.data_ptr(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            _lib.check("bt_gqa_decode_split", rc)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "pmc", "copy_bytes_each_way": src.numel() * 2,
+                      "split_algorithmic_bytes": 2 * L * HKV * D * 2 + H * D * 4}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -73,6 +119,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--mode", choices=["bench", "pmc"], default="bench",
+                    help="pmc: only a 256 MiB device copy and the config-2 split kernel, "
+                         "5 launches each, for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print("this build measures one GPU only: the decode/prefill kernels run on a single "
@@ -94,6 +143,8 @@ def main() -> int:
     backend = HipBackend(dev)
     log(f"{backend!r}")
     H, HKV, D, CAP = 8, 2, 256, 65536
+    if args.mode == "pmc":
+        return pmc_mode(torch, backend, dev)
 
     def fixed_case(case, cap):
         cache = KVCache(cap, case.k.shape[1], case.k.shape[2], dev)
@@ -104,33 +155,50 @@ def main() -> int:
         pos = torch.tensor([case.pos], dtype=torch.int32, device=dev)
         return cache, q, kv, vv, pos
 
-    def decode_point(case, cap, steps, warmup, check=False):
-        cache, q, kv, vv, pos = fixed_case(case, cap)
+    def decode_point(case, cap, steps, warmup, n_layers=6, check=False):
+        """µs per call with one graph holding one call per distinct layer cache."""
+        lay = [fixed_case(case, cap) for _ in range(n_layers)]
         heads = case.q.shape[0]
-        ms = time_graph(torch, lambda: backend.attention_fixed(q, kv, vv, pos, case.scale), steps, warmup)
-        nbytes = wl.decode_bytes(case.valid, heads, kv.shape[1], kv.shape[2])
+
+        def run():
+            for _, lq, lk, lv, lp in lay:
+                backend.attention_fixed(lq, lk, lv, lp, case.scale)
+
+        ms = time_graph(torch, run, steps, warmup) / n_layers
+        nbytes = wl.decode_bytes(case.valid, heads, case.k.shape[1], case.k.shape[2])
         res = {"valid": case.valid, "us_per_call": ms * 1e3, "GBps": nbytes / (ms * 1e-3) / 1e9,
-               "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes": nbytes}
+               "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes": nbytes,
+               "layer_caches": n_layers}
         if check:
             from oracle.attention import compare, fixed_decode  # checker only
 
-            out = backend.attention_fixed(q, kv, vv, pos, case.scale).cpu()
+            _, lq, lk, lv, lp = lay[-1]
+            out = backend.attention_fixed(lq, lk, lv, lp, case.scale).cpu()
             ref = fixed_decode(case.q.float(), case.k.float(), case.v.float(), case.pos, case.scale)
             err, cos = compare(out.numpy(), ref.numpy())
             res["parity"] = {"max_abs": err, "cosine": cos}
-        del cache
+        del lay
+        torch.cuda.empty_cache()
         return res
 
     # ---------------------------------------------------------------- headline
     L = 32768
-    log(f"config 2 headline: H={H} Hkv={HKV} D={D} cap={CAP} valid={L}")
+    LAYERS = 6  # attention layers of the 0.8B decoder: (i + 1) % 4 == 0 of 24 (config.py:37-39)
+    log(f"config 2 headline: H={H} Hkv={HKV} D={D} cap={CAP} valid={L}, {LAYERS} layer caches")
     head_case = wl.c2_inputs(L, cap=CAP)
-    cache, q, kv, vv, pos = fixed_case(head_case, CAP)
-    step = lambda: backend.attention_fixed(q, kv, vv, pos, head_case.scale)  # noqa: E731
-    ms_per_step = time_graph(torch, step, args.steps, args.warmup)
+    layers = [fixed_case(head_case, CAP) for _ in range(LAYERS)]
+    q, kv, vv, pos = layers[0][1], layers[0][2], layers[0][3], layers[0][4]
+
+    def decode_step():
+        for _, lq, lk, lv, lp in layers:
+            backend.attention_fixed(lq, lk, lv, lp, head_case.scale)
+
+    ms_per_step = time_graph(torch, decode_step, args.steps, args.warmup, calls_per_graph=1) / LAYERS
     nbytes = wl.decode_bytes(L, H, HKV, D)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     log(f"headline: {ms_per_step * 1e3:.2f} us/call, {value:.0f} GB/s")
+    single_ms = time_graph(torch, lambda: backend.attention_fixed(q, kv, vv, pos, head_case.scale),
+                           args.steps, args.warmup)
 
     # ---- roofline: the split kernel alone, HIP events on its stream ----------
     lib = _lib.lib()
@@ -139,14 +207,16 @@ def main() -> int:
     part = torch.empty((H, ns, D), dtype=torch.float32, device=dev)
 
     def split_only():
-        rc = lib.bt_gqa_decode_split(
-            q.data_ptr(), _lib.BT_DTYPE_F32, H * D, kv.data_ptr(), vv.data_ptr(), kv.stride(0),
-            kv.stride(1), None, pos.data_ptr(), None, 0, 1, H, HKV, D, ns, head_case.scale,
-            lse.data_ptr(), part.data_ptr(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
-        )
-        _lib.check("bt_gqa_decode_split", rc)
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for _, lq, lk, lv, lp in layers:
+            rc = lib.bt_gqa_decode_split(
+                lq.data_ptr(), _lib.BT_DTYPE_F32, H * D, lk.data_ptr(), lv.data_ptr(), lk.stride(0),
+                lk.stride(1), None, lp.data_ptr(), None, CAP, 1, H, HKV, D, ns, head_case.scale,
+                lse.data_ptr(), part.data_ptr(), stream,
+            )
+            _lib.check("bt_gqa_decode_split", rc)
 
-    split_ms = time_graph(torch, split_only, args.steps, args.warmup, calls_per_graph=20)
+    split_ms = time_graph(torch, split_only, args.steps, args.warmup, calls_per_graph=1) / LAYERS
     split_bytes = 2 * L * HKV * D * 2 + H * D * 4  # K + V of the valid prefix, q once
     achieved = split_bytes / (split_ms * 1e-3) / 1e9
     log(f"split kernel: {split_ms * 1e3:.2f} us, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})")
@@ -160,6 +230,8 @@ def main() -> int:
                 "algorithmic_bytes": split_bytes, "num_split": ns}
 
     extra: dict = {"headline_us_per_call": round(ms_per_step * 1e3, 3), "num_split": ns,
+                   "single_call_graph": {"us_per_call": round(single_ms * 1e3, 3),
+                                         "GBps": round(nbytes / (single_ms * 1e-3) / 1e9, 1)},
                    "num_cus": backend.num_cus, "arch": backend.arch}
     # --------------------------------------------------------------- extras
     if not args.no_extra:
@@ -168,36 +240,33 @@ def main() -> int:
                        for v in (1024, 4096, 32768)]
         log("c2 sweep: " + ", ".join(f"{r['valid']}: {r['us_per_call']:.2f}us {r['GBps']:.0f}GB/s"
                                      for r in extra["c2"]))
-        # cold: 5 distinct caches (>256 MB Infinity Cache), one call each per replay
-        caches = [fixed_case(head_case, CAP) for _ in range(5)]
-        def cold():
-            for c in caches:
-                backend.attention_fixed(c[1], c[2], c[3], c[4], head_case.scale)
-        cold_ms = time_graph(torch, cold, esteps, ewarm) / 5
-        extra["c2_cold_32k"] = {"us_per_call": cold_ms * 1e3, "GBps": nbytes / (cold_ms * 1e-3) / 1e9,
-                                "frac_hbm_peak": nbytes / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                                "caches": 5}
-        log(f"c2 cold 32k: {cold_ms * 1e3:.2f} us/call")
-        del caches
+        # hot: the same cache 6 times per graph, so the 64 MiB prefix stays in the Infinity Cache
+        hot_ms = time_graph(torch, lambda: [backend.attention_fixed(q, kv, vv, pos, head_case.scale)
+                                            for _ in range(LAYERS)], esteps, ewarm) / LAYERS
+        extra["c2_mall_hot_32k"] = {"us_per_call": hot_ms * 1e3, "GBps": nbytes / (hot_ms * 1e-3) / 1e9}
+        log(f"c2 MALL-hot 32k: {hot_ms * 1e3:.2f} us/call")
+        del layers
+        torch.cuda.empty_cache()
         c3 = []
         for v in (8192, 32768, 131072):
-            c3.append(decode_point(wl.c3_inputs(v, cap=131072), 131072, esteps, ewarm))
+            c3.append(decode_point(wl.c3_inputs(v, cap=131072), 131072, esteps, ewarm, check=v < 131072))
         extra["c3"] = c3
         log("c3: " + ", ".join(f"{r['valid']}: {r['us_per_call']:.2f}us {r['GBps']:.0f}GB/s" for r in c3))
         # ragged (config 5)
         rc5 = wl.c5_inputs()
         rq = rc5.q.float().to(dev)
-        rk, rv = rc5.k.to(dev), rc5.v.to(dev)
+        rkv = [(rc5.k.to(dev), rc5.v.to(dev)) for _ in range(3)]  # 3 layer caches, ~1 GB
         roff = torch.tensor(rc5.offsets, dtype=torch.int64, device=dev)
         rlen = torch.tensor(rc5.lens, dtype=torch.int32, device=dev)
-        rms = time_graph(torch, lambda: backend.attention_ragged(rq, rk, rv, roff, rlen, rc5.lens, rc5.scale),
-                         esteps, ewarm)
+        rms = time_graph(torch, lambda: [backend.attention_ragged(rq, rk, rv, roff, rlen, rc5.lens, rc5.scale)
+                                         for rk, rv in rkv], esteps, ewarm) / len(rkv)
         rbytes = 2 * sum(rc5.lens) * HKV * D * 2 + len(rc5.lens) * H * D * 4 * 2
         extra["c5_ragged"] = {"us_per_call": rms * 1e3, "GBps": rbytes / (rms * 1e-3) / 1e9,
                               "frac_hbm_peak": rbytes / (rms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                               "tokens": sum(rc5.lens), "bytes": rbytes}
         log(f"c5 ragged: {rms * 1e3:.2f} us/call")
-        del rk, rv
+        del rkv
+        torch.cuda.empty_cache()
         # prefill (config 4), if served
         pre = []
         for s in (128, 512, 2048, 8192):

@@ -28,6 +28,7 @@ _vp = ctypes.c_void_p
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "bt_version": (ctypes.c_int, []),
     "bt_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "bt_decode_tile_tokens": (_c_i32, []),
     "bt_decode_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32]),
     "bt_decode_pick_splits": (_c_i32, [_c_i32, _c_i32, _c_i32]),
     "bt_gqa_decode_split": (

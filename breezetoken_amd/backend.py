@@ -88,6 +88,11 @@ class HipBackend:
             self._ws[key] = ws  # kept until close(): captured graphs may point at it
         return ws
 
+    @property
+    def tile_tokens(self) -> int:
+        """Tokens per decode tile; tile t belongs to split t % num_split."""
+        return int(self._lib.bt_decode_tile_tokens())
+
     def pick_splits(self, kv_heads: int, ctx_len: int) -> int:
         return int(self._lib.bt_decode_pick_splits(kv_heads, ctx_len, self.num_cus))
 
@@ -105,6 +110,8 @@ class HipBackend:
             raise RuntimeError("k/v need unit d-stride and identical strides")
         if dim not in SERVED_HEAD_DIMS or heads // groups > MAX_GROUP:
             raise RuntimeError(f"shape H={heads} Hkv={groups} D={dim} is not served")
+        if k.shape[0] * k.stride(0) * 2 >= 1 << 32:
+            raise RuntimeError("one sequence's KV extent must stay below 4 GiB")
         return groups
 
     # ----------------------------------------------------------- decode (eager)
@@ -137,7 +144,8 @@ class HipBackend:
             pos = pos.reshape(1).to(torch.int32)  # as backends.py:561
         if pos.device != self._dev:
             raise RuntimeError("pos must be a device tensor")
-        return self._decode(q, k, v, scale, groups, seqlen=0, pos=pos.reshape(-1)[:1], ctx=k.shape[0])
+        return self._decode(q, k, v, scale, groups, seqlen=k.shape[0], pos=pos.reshape(-1)[:1],
+                            ctx=k.shape[0])
 
     def _decode(self, q, k, v, scale, groups, *, seqlen: int, pos, ctx: int) -> torch.Tensor:
         heads, dim = q.shape
@@ -173,7 +181,7 @@ class HipBackend:
         rc = self._lib.bt_gqa_decode_split(
             q.data_ptr(), _dtype_code(q.dtype), heads * dim,
             k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
-            None, _ptr(pos), None, 0 if pos is not None else k.shape[0],
+            None, _ptr(pos), None, k.shape[0],
             1, heads, groups, dim, num_split, float(scale),
             lse.data_ptr(), part.data_ptr(), _stream(self._dev),
         )
@@ -207,7 +215,7 @@ class HipBackend:
         rc = self._lib.bt_gqa_decode(
             q.data_ptr(), _dtype_code(q.dtype), heads * dim,
             k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
-            seq_offset.data_ptr(), pos.data_ptr(), None, 0,
+            seq_offset.data_ptr(), pos.data_ptr(), None, k.shape[0],
             batch, heads, groups, dim, ns, float(scale),
             ws.data_ptr(), ws.numel(), out.data_ptr(), BT_DTYPE_F32, heads * dim,
             _stream(self._dev),

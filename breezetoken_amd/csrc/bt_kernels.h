@@ -6,8 +6,14 @@
 
 namespace bt {
 
-// Largest number of splits one sequence may use (LSE weights live in LDS).
+// Largest number of splits one sequence may use.
 constexpr int kMaxSplitsPerSeq = 4096;
+
+// Tokens per decode tile (the unit dealt round-robin to splits).
+#ifndef BT_DECODE_TILE
+#define BT_DECODE_TILE 16
+#endif
+constexpr int kDecodeTileTokens = BT_DECODE_TILE;
 
 struct DecodeSplitParams {
   const void* q;             // (batch, heads, D) f32 or bf16; head stride = D
@@ -20,12 +26,13 @@ struct DecodeSplitParams {
   const int64_t* seq_offset; // (batch,) first slot of each sequence, or null (0)
   const int32_t* pos;        // (batch,) valid = pos + 1, or null
   const int32_t* seq_len;    // (batch,) valid lengths, or null
-  int32_t seqlen;            // valid length when pos and seq_len are null
+  int32_t seqlen;            // valid length when pos and seq_len are null; capacity when pos is set
   const int4* work;          // (num_work,) {b, s, ns_b, base_b}, or null: uniform num_split
   int32_t num_split;
   int32_t total_splits;      // row length of lse / part per head
   int32_t heads;
   int32_t kv_heads;
+  int32_t group;             // heads / kv_heads
   float scale_log2;          // softmax scale * log2(e)
   float* lse;                // (heads, total_splits)
   float* part;               // (heads, total_splits, D)
@@ -57,6 +64,24 @@ struct PrefillParams {
   int out_bf16;
   int64_t out_stride_tok, out_stride_head;
 };
+
+// Which kernel variant serves a combination of length sources, or -1 if the
+// combination is not served:
+//   work table (ragged)              -> needs seq_len and seq_offset, no pos
+//   pos, batch 1, no seq_offset      -> single sequence, device position
+//   pos + seq_offset                 -> batch of device positions
+//   seq_len + seq_offset             -> batch of device lengths
+//   none of them, batch 1            -> explicit length argument
+inline int decode_mode(bool work, bool pos, bool seq_len, bool seq_offset, int batch) {
+  if (work) return (seq_len && seq_offset && !pos) ? 3 : -1;
+  if (pos) {
+    if (seq_len) return -1;
+    if (!seq_offset) return batch == 1 ? 1 : -1;
+    return 2;
+  }
+  if (seq_len) return seq_offset ? 4 : -1;
+  return (batch == 1 && !seq_offset) ? 0 : -1;
+}
 
 hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int grid_x, int batch,
                                hipStream_t stream);

@@ -62,6 +62,7 @@ bt::DecodeSplitParams make_split_params(const void* q, int32_t q_dtype, int64_t 
   p.seqlen = seqlen;
   p.heads = heads;
   p.kv_heads = kv_heads;
+  p.group = heads / kv_heads;
   p.scale_log2 = (float)((double)scale * kLog2e);
   p.lse = lse;
   p.part = part;
@@ -85,6 +86,8 @@ const char* bt_strerror(int code) {
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
 }
+
+int32_t bt_decode_tile_tokens(void) { return bt::kDecodeTileTokens; }
 
 int64_t bt_decode_workspace_bytes(int32_t heads, int32_t head_dim, int32_t total_splits) {
   if (heads < 1 || head_dim < 1 || total_splits < 1) return 0;
@@ -115,6 +118,10 @@ int bt_gqa_decode_split(const void* q, int32_t q_dtype, int64_t q_stride_seq, co
   if (num_split < 1) return BT_EINVAL;
   if (num_split > bt::kMaxSplitsPerSeq) return BT_ENOTSUP;
   if (!pos && !seq_len && seqlen < 0) return BT_EINVAL;
+  if (pos && seqlen < 1) return BT_EINVAL;  // capacity bound for the position path
+  if (bt::decode_mode(false, pos != nullptr, seq_len != nullptr, seq_offset != nullptr, batch) < 0)
+    return BT_EINVAL;
+  if ((int64_t)seqlen * kv_stride_tok * 2 > (int64_t)UINT32_MAX) return BT_ENOTSUP;
   if ((int64_t)batch * num_split > INT32_MAX / 2) return BT_ENOTSUP;
   bt::DecodeSplitParams p = make_split_params(q, q_dtype, q_stride_seq, k, v, kv_stride_tok,
                                               kv_stride_head, seq_offset, pos, seq_len, seqlen,

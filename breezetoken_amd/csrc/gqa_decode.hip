@@ -1,25 +1,28 @@
 // Split-KV GQA flash-decode for gfx950 (MI355X) over a bf16 token-major KV cache.
 //
 // Semantics follow the reference split kernel (breezetoken/kernels/cuda/
-// attention.py:88-166, fixed-capacity variant 249-326): the valid context of a
-// sequence is cut into 32-token tiles, split s of NS owns tiles
-// [s*base + min(s, extra), +base + (s < extra)) (attention.py:106-112), and each
-// split writes, per query head, a log2-domain LSE
+// attention.py:88-166, fixed-capacity variant 249-326): the valid context is cut
+// into tiles, every split writes, per query head, a log2-domain LSE
 //     lse = log2(l) + m,   l = sum_j exp2(x_j - m),   x_j = q.k_j * scale * log2e
-// and the normalised partial output sum_j exp2(x_j - m) v_j / l.  An empty split
-// writes lse = -inf and leaves its partial untouched (the combine never reads it).
+// and the normalised partial output sum_j exp2(x_j - m) v_j / l (attention.py:
+// 153-166); an empty split writes lse = -inf and leaves its partial untouched
+// (the combine never reads it).  One deliberate difference: tiles are dealt to
+// splits round-robin (tile t -> split t mod NS) instead of in contiguous ranges
+// (attention.py:106-112).  The LSE combine is invariant to how tokens are
+// partitioned, and with round-robin dealing a split's first tile (tile s) is
+// known before the position tensor is read, so its loads start at kernel entry.
 //
 // Work decomposition (MI355X-first, not the reference's):
-//  * one work-group (4 waves) per (split, kv head, sequence); the group's G query
-//    heads ride in the N dimension of v_mfma_f32_16x16x32_bf16, so every K/V byte
-//    fetched from HBM is used by all G heads;
+//  * one work-group (WAVES waves) per (split, kv head, sequence); the group's G
+//    query heads ride in the N dimension of the MFMA, so every K/V byte fetched
+//    from HBM is used by all G heads;
 //  * q is pre-scaled by scale*log2e and split into bf16 hi + lo columns (columns
 //    h and 2*GMAX-1-h), so Q.K^T keeps ~16 mantissa bits although the MFMA takes
 //    bf16; the two halves are summed with one DPP mirror.  P is split the same
 //    way for the P.V product;
 //  * S^T = K . Q^T puts the K tile in the A operand, so K rows go straight from
-//    HBM into registers with 16-byte loads (64 contiguous bytes per token per
-//    instruction);
+//    HBM into registers with 16-byte buffer loads (64 contiguous bytes per token
+//    per instruction); loads past the valid length return zero (buffer bounds);
 //  * V is staged through an XOR-swizzled LDS tile per wave and read back with
 //    ds_read_b64_tr_b16, which yields the V^T operand of O^T = V^T . P^T without
 //    any shuffle; the lane that owns score column n for tokens t also owns the
@@ -37,70 +40,111 @@ namespace bt {
 
 namespace {
 
-constexpr int kTile = 32;      // tokens per tile (the P.V MFMA's K dimension)
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-
 __device__ __forceinline__ int swz(int row, int slots) { return ((row & 7) * 2) & (slots - 1); }
 
-template <int GMAX, int D>
-struct DecodeTile {
-  static constexpr int kSteps = D / 32;      // K-dimension steps of Q.K^T
-  static constexpr int kDTiles = D / 16;     // 16-wide d tiles of O^T
-  static constexpr int kSlots = D / 8;       // 16-byte chunks per row
-  static constexpr int kVLoads = D / 16;     // 1 KiB wave loads per V tile
-  static constexpr int kRowBytes = D * 2;
-  static constexpr int kVTileBytes = kTile * kRowBytes;
+// Raw buffer resource over [base, base + bytes): loads past the end return 0,
+// so tokens past the valid length need no clamping.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+}
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// Scalar (constant-cache) read of a wave-uniform value written by an earlier
+// kernel: issued as s_load, so its wait lands at the first use instead of
+// forcing a vector load + readfirstlane right away.
+template <typename T>
+__device__ __forceinline__ T uniform_load(const T* p, int i) {
+  return ((const __attribute__((address_space(4))) T*)(p))[i];
+}
+
+__device__ __forceinline__ floatx4 mfma16k16(const u32x2& a, const u32x2& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, a),
+                                                  __builtin_bit_cast(short4_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x2 lds_read_tr4(const BT_LDS uint16_t* p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((BT_LDS bf16x4*)p));
+}
+
+template <int GMAX>
+__device__ __forceinline__ float mirror(float v) {
+  return (GMAX <= 4) ? dpp_f32<DPP_ROW_HALF_MIRROR>(v) : dpp_f32<DPP_ROW_MIRROR>(v);
+}
+
+}  // namespace
+
+// Where the valid length of a sequence comes from.  Each mode is its own
+// kernel, so the prologue has no argument-dependent branches and all kernel
+// arguments arrive in one batch of scalar loads.
+enum DecodeMode : int {
+  kModeLen = 0,       // explicit length argument (eager decode)
+  kModePos = 1,       // device position of one sequence (graph decode)
+  kModePosBatch = 2,  // device positions + first slots of a batch in one cache
+  kModeRagged = 3,    // work table + device lengths + first slots
+  kModeLenBatch = 4,  // device lengths + first slots, uniform split count
 };
 
-template <int GMAX, int D>
-__global__ __launch_bounds__(kThreads, 1) void gqa_decode_split_kernel(DecodeSplitParams p) {
-  using T = DecodeTile<GMAX, D>;
-  constexpr int kSteps = T::kSteps;
-  constexpr int kDTiles = T::kDTiles;
-  constexpr int kSlots = T::kSlots;
-  constexpr int kVLoads = T::kVLoads;
-  constexpr int kRowBytes = T::kRowBytes;
+// GMAX: 4 (groups of <= 4 query heads) or 8; D: head dim; WAVES: waves per
+// work-group; TILE: tokens a wave processes per step (16 or 32); PIPE: 1 =
+// one register buffer whose next tile is fetched as soon as it is consumed,
+// 2 = two register buffers (next tile in flight during the current one);
+// MODE: a DecodeMode; QBF16: q is bf16 (else f32).
+template <int GMAX, int D, int WAVES, int TILE, int PIPE, int MODE, bool QBF16>
+__global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeSplitParams p) {
+  constexpr int kThreads = WAVES * 64;
+  constexpr int kSteps = D / 32;            // K-dimension steps of Q.K^T
+  constexpr int kSub = TILE / 16;           // 16-token sub-tiles of S^T
+  constexpr int kDTiles = D / 16;           // 16-wide d tiles of O^T
+  constexpr int kSlots = D / 8;             // 16-byte chunks per row
+  constexpr int kRowBytes = D * 2;
+  constexpr int kVTileBytes = TILE * kRowBytes;
+  constexpr int kVLoads = kVTileBytes / 1024;  // 1 KiB wave loads per V tile
+  constexpr int kRowsPerLoad = 1024 / kRowBytes;
+  constexpr int kSwzPeriod = 8 / kRowsPerLoad > 0 ? 8 / kRowsPerLoad : 1;
+  static_assert(TILE == 16 || TILE == 32, "tile is 16 or 32 tokens");
+  static_assert(kVLoads >= 1, "V tile must fill at least one wave load");
 
   // LDS: one V tile per wave; reused for the cross-wave merge at the end.
-  constexpr int kMergeBytes = kWaves * GMAX * (D + 2) * 4;
-  constexpr int kVBytes = kWaves * T::kVTileBytes;
+  constexpr int kMergeBytes = WAVES * GMAX * (D + 2) * 4;
+  constexpr int kVBytes = WAVES * kVTileBytes;
   constexpr int kLdsBytes = kVBytes > kMergeBytes ? kVBytes : kMergeBytes;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kLdsBytes];
+  // Q^T operand, identical for every wave: [step][lane] 16-byte fragments.
+  __shared__ __attribute__((aligned(16))) u32x4 qlds[kSteps * 64];
 
+  // Every kernel argument lands in SGPRs in one batch of scalar loads here,
+  // instead of lazily inside branches (each lazy batch is a memory round trip).
+  asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.v), "s"(p.pos), "s"(p.seq_len), "s"(p.seq_offset),
+               "s"(p.work), "s"(p.seqlen), "s"(p.num_split), "s"(p.total_splits), "s"(p.group),
+               "s"(p.kv_stride_tok), "s"(p.kv_stride_head), "s"(p.q_stride_seq), "s"(p.scale_log2),
+               "s"(p.lse), "s"(p.part));
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kvh = blockIdx.y;
-  const int G = p.heads / p.kv_heads;
+  const int G = p.group;
 
   int b, s, ns, base;
-  if (p.work != nullptr) {
-    const int4 w = p.work[blockIdx.x];
-    b = w.x; s = w.y; ns = w.z; base = w.w;
+  if constexpr (MODE == kModeRagged) {
+    const int* w = reinterpret_cast<const int*>(p.work) + 4 * (int)blockIdx.x;
+    b = uniform_load(w, 0); s = uniform_load(w, 1); ns = uniform_load(w, 2); base = uniform_load(w, 3);
   } else {
     b = blockIdx.z; s = blockIdx.x; ns = p.num_split; base = b * p.num_split;
   }
-
-  int valid;
-  if (p.pos != nullptr) valid = p.pos[b] + 1;
-  else if (p.seq_len != nullptr) valid = p.seq_len[b];
-  else valid = p.seqlen;
-  if (valid < 0) valid = 0;
-  const int64_t seq_off = p.seq_offset != nullptr ? p.seq_offset[b] : 0;
-
-  // Split partition (attention.py:106-112).
-  const int tiles = (valid + kTile - 1) / kTile;
-  const int tbase = tiles / ns, extra = tiles % ns;
-  const int n_tiles = tbase + (s < extra ? 1 : 0);
-  const int tile0 = s * tbase + (s < extra ? s : extra);
+  // The length source is read first so its round trip overlaps the q and
+  // K/V loads issued below.
+  int len_raw;
+  if constexpr (MODE == kModePos || MODE == kModePosBatch) len_raw = uniform_load(p.pos, b) + 1;
+  else if constexpr (MODE == kModeRagged || MODE == kModeLenBatch) len_raw = uniform_load(p.seq_len, b);
+  else len_raw = p.seqlen;
+  int64_t seq_off = 0;
+  if constexpr (MODE != kModeLen && MODE != kModePos) seq_off = uniform_load(p.seq_offset, b);
 
   const int head0 = kvh * G;
   const int split_idx = base + s;
-
-  if (n_tiles == 0) {
-    if (threadIdx.x < G) p.lse[(int64_t)(head0 + threadIdx.x) * p.total_splits + split_idx] = -INFINITY;
-    return;
-  }
 
   // ---- column roles: hi column h < G, lo column 2*GMAX-1-h ----------------
   const int col = lane & 15;
@@ -113,41 +157,63 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_decode_split_kernel(DecodeSpl
     col_head = 2 * GMAX - 1 - col;
     col_lo = true;
   }
+  // Branch-free operand selection: keep_hi / keep_lo are all-ones or zero.
+  const uint32_t keep_hi = (col_head >= 0 && !col_lo) ? 0xffffu : 0u;
+  const uint32_t keep_lo = col_lo ? 0xffffu : 0u;
 
-  // ---- Q^T operand: bf16 hi or lo of q*scale*log2e ------------------------
-  bf16x8 qop[kSteps];
-  {
-    const int64_t qrow = (int64_t)b * p.q_stride_seq + (int64_t)(head0 + (col_head < 0 ? 0 : col_head)) * D;
+  // ---- wave 0 issues the q loads first: they do not depend on the length ----
+  const int64_t qrow = (int64_t)b * p.q_stride_seq + (int64_t)(head0 + (col_head < 0 ? 0 : col_head)) * D;
+  u32x4 qraw[kSteps][2];
+  if (wave == 0) {
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
       const int d0 = (st * 4 + kg) * 8;
-      float qv[8];
-      if (p.q_bf16) {
-        const u32x4 raw = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(p.q) + qrow + d0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          qv[2 * i] = bf16_bits_to_f32(raw[i] & 0xffffu);
-          qv[2 * i + 1] = bf16_bits_to_f32(raw[i] >> 16);
-        }
+      if constexpr (QBF16) {
+        qraw[st][0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(p.q) + qrow + d0);
       } else {
-        const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.q) + qrow + d0);
-        const float4 c = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.q) + qrow + d0 + 4);
-        qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w;
-        qv[4] = c.x; qv[5] = c.y; qv[6] = c.z; qv[7] = c.w;
+        qraw[st][0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.q) + qrow + d0);
+        qraw[st][1] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.q) + qrow + d0 + 4);
       }
-      uint32_t h16[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float x = qv[i] * p.scale_log2;
-        const uint32_t hi = f32_to_bf16_bits(x);
-        const uint32_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
-        h16[i] = col_head < 0 ? 0u : (col_lo ? lo : hi);
-      }
-      const u32x4 packed = {pack2(h16[0], h16[1]), pack2(h16[2], h16[3]), pack2(h16[4], h16[5]),
-                            pack2(h16[6], h16[7])};
-      qop[st] = as_bf16x8(packed);
     }
   }
+
+  // ---- K/V addressing -------------------------------------------------------
+  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+  unsigned char* vtile = smem + wave * kVTileBytes;
+
+  uint32_t koff[kSub];
+#pragma unroll
+  for (int sub = 0; sub < kSub; ++sub) koff[sub] = (uint32_t)(sub * 16 + col) * row_bytes + kg * 16;
+  uint32_t voff[kSwzPeriod];
+#pragma unroll
+  for (int j = 0; j < kSwzPeriod; ++j) {
+    const int r = j * kRowsPerLoad + lane / kSlots;
+    const int c = (lane % kSlots) ^ swz(r, kSlots);
+    voff[j] = (uint32_t)r * row_bytes + c * 16;
+  }
+
+  // Speculative path (device position, single sequence): the split's first
+  // tile is tile s, so wave 0 fetches it inside the capacity bound before the
+  // position is known.  Slots in [valid, capacity) are masked after it arrives.
+  constexpr bool speculate = MODE == kModePos;
+  const int64_t head_off0 = (int64_t)kvh * p.kv_stride_head;
+  __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + head_off0, (uint32_t)p.seqlen * row_bytes);
+  __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.v + head_off0, (uint32_t)p.seqlen * row_bytes);
+
+  auto load_k = [&](int tile, u32x4 (&kr)[kSub][kSteps]) {
+    const uint32_t so = (uint32_t)tile * TILE * row_bytes;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st)
+#pragma unroll
+      for (int sub = 0; sub < kSub; ++sub) kr[sub][st] = buf_load16(krs, koff[sub] + st * 64, so);
+  };
+  auto load_v = [&](int tile, u32x4 (&vr)[kVLoads]) {
+    const uint32_t so = (uint32_t)tile * TILE * row_bytes;
+#pragma unroll
+    for (int j = 0; j < kVLoads; ++j)
+      vr[j] = buf_load16(vrs, voff[j % kSwzPeriod],
+                         so + (uint32_t)(j / kSwzPeriod) * (kSwzPeriod * kRowsPerLoad) * row_bytes);
+  };
 
   // ---- per-wave state -------------------------------------------------------
   floatx4 oacc[kDTiles];
@@ -156,125 +222,212 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_decode_split_kernel(DecodeSpl
   float m_run = -INFINITY;
   float l_run = 0.f;
 
-  const uint16_t* kbase = p.k + seq_off * p.kv_stride_tok + (int64_t)kvh * p.kv_stride_head;
-  const uint16_t* vbase = p.v + seq_off * p.kv_stride_tok + (int64_t)kvh * p.kv_stride_head;
-  unsigned char* vtile = smem + wave * T::kVTileBytes;
-  const int last = valid - 1;
+  u32x4 kr[PIPE][kSub][kSteps];
+  u32x4 vr[PIPE][kVLoads];
+  const bool spec_loaded = speculate && wave == 0;
+  if (spec_loaded) {
+    load_k(s, kr[0]);
+    load_v(s, vr[0]);
+  }
 
-  auto load_k = [&](int tile, u32x4 (&kr)[2][kSteps]) {
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      int t = tile * kTile + sub * 16 + col;
-      t = t > last ? last : t;
-      const uint16_t* row = kbase + (int64_t)t * p.kv_stride_tok + kg * 8;
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) kr[sub][st] = *reinterpret_cast<const u32x4*>(row + st * 32);
-    }
-  };
-  auto load_v = [&](int tile, u32x4 (&vr)[kVLoads]) {
-#pragma unroll
-    for (int j = 0; j < kVLoads; ++j) {
-      const int pbyte = j * 1024 + lane * 16;
-      const int r = pbyte / kRowBytes;
-      const int slot = (pbyte % kRowBytes) / 16;
-      const int c = slot ^ swz(r, kSlots);
-      int t = tile * kTile + r;
-      t = t > last ? last : t;
-      vr[j] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)t * p.kv_stride_tok + c * 8);
-    }
-  };
+  // ---- valid length (device position, length table or argument) ------------
+  int valid = len_raw;
+  if constexpr (MODE == kModePos || MODE == kModePosBatch) {
+    if (valid > p.seqlen) valid = p.seqlen;  // seqlen carries the capacity here
+  }
+  if (valid < 0) valid = 0;
+  if constexpr (!speculate) {
+    const int64_t head_off = seq_off * p.kv_stride_tok + head_off0;
+    krs = make_rsrc(p.k + head_off, (uint32_t)valid * row_bytes);
+    vrs = make_rsrc(p.v + head_off, (uint32_t)valid * row_bytes);
+  }
 
-  auto compute = [&](int tile, bool has_next, u32x4 (&kr)[2][kSteps], u32x4 (&vr)[kVLoads]) {
-    // S^T = K . Q^T for two 16-token sub-tiles.
-    floatx4 sacc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+  // Round-robin partition: tile t belongs to split t % ns; inside the split,
+  // wave w takes the split's tiles w, w + WAVES, ...
+  const int tiles = (valid + TILE - 1) / TILE;
+  const int n_tiles = tiles > s ? (tiles - s + ns - 1) / ns : 0;
+  if (n_tiles == 0) {
+    if (threadIdx.x < G) p.lse[(int64_t)(head0 + threadIdx.x) * p.total_splits + split_idx] = -INFINITY;
+    return;
+  }
+  const int my_tiles = n_tiles > wave ? (n_tiles - wave + WAVES - 1) / WAVES : 0;
+  const int tstride = ns * WAVES;        // tile distance between a wave's steps
+  const int tfirst = s + ns * wave;      // this wave's first tile
+  if (my_tiles > 0) {
+    if (!spec_loaded) {
+      load_k(tfirst, kr[0]);
+      load_v(tfirst, vr[0]);
+    }
+    if (PIPE == 2 && my_tiles > 1) {
+      load_k(tfirst + tstride, kr[PIPE - 1]);
+      load_v(tfirst + tstride, vr[PIPE - 1]);
+    }
+  }
+
+  // ---- wave 0 builds the Q^T operand (bf16 hi or lo of q*scale*log2e) -------
+  if (wave == 0) {
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
-      sacc[0] = mfma16(as_bf16x8(kr[0][st]), qop[st], sacc[0]);
-      sacc[1] = mfma16(as_bf16x8(kr[1][st]), qop[st], sacc[1]);
-    }
-    // K registers are free again: start fetching the next tile's K.
-    if (has_next) load_k(tile + kWaves, kr);
-    // Stage V into this wave's swizzled LDS tile (same-wave LDS ops stay ordered),
-    // then reuse the V registers for the next tile's V.
+      float qv[8];
+      if constexpr (QBF16) {
 #pragma unroll
-    for (int j = 0; j < kVLoads; ++j)
-      *reinterpret_cast<BT_LDS u32x4*>((BT_LDS unsigned char*)vtile + j * 1024 + lane * 16) = vr[j];
-    if (has_next) load_v(tile + kWaves, vr);
+        for (int i = 0; i < 4; ++i) {
+          qv[2 * i] = bf16_bits_to_f32(qraw[st][0][i] & 0xffffu);
+          qv[2 * i + 1] = bf16_bits_to_f32(qraw[st][0][i] >> 16);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qv[i] = __uint_as_float(qraw[st][0][i]);
+          qv[4 + i] = __uint_as_float(qraw[st][1][i]);
+        }
+      }
+      uint32_t h16[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float x = qv[i] * p.scale_log2;
+        const uint32_t hi = f32_to_bf16_bits(x);
+        const uint32_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
+        h16[i] = (hi & keep_hi) | (lo & keep_lo);
+      }
+      const u32x4 packed = {pack2(h16[0], h16[1]), pack2(h16[2], h16[3]), pack2(h16[4], h16[5]),
+                            pack2(h16[6], h16[7])};
+      qlds[st * 64 + lane] = packed;
+    }
+  }
+  __syncthreads();
+
+  const int i16 = lane & 15;
+  auto compute = [&](int tile, bool fetch_next, u32x4 (&k)[kSub][kSteps], u32x4 (&v)[kVLoads]) {
+    // S^T = K . Q^T, one 16-token sub-tile per accumulator.
+    floatx4 sacc[kSub];
+#pragma unroll
+    for (int sub = 0; sub < kSub; ++sub) sacc[sub] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // Re-read Q^T from LDS every tile instead of pinning 32 VGPRs for the whole loop.
+    asm volatile("" ::: "memory");
+    u32x4 qop[kSteps];
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) qop[st] = qlds[st * 64 + lane];
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+#pragma unroll
+      for (int sub = 0; sub < kSub; ++sub)
+        sacc[sub] = mfma16(as_bf16x8(k[sub][st]), as_bf16x8(qop[st]), sacc[sub]);
+    }
+    if (PIPE == 1 && fetch_next) load_k(tile + tstride, k);
+    // Stage V into this wave's swizzled LDS tile (same-wave LDS ops stay ordered).
+    // Rows past the valid length become zeros: P is 0 there, but 0 * NaN is not.
+#pragma unroll
+    for (int j = 0; j < kVLoads; ++j) {
+      const int r = (j / kSwzPeriod) * (kSwzPeriod * kRowsPerLoad) + (j % kSwzPeriod) * kRowsPerLoad + lane / kSlots;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<BT_LDS u32x4*>((BT_LDS unsigned char*)vtile + j * 1024 + lane * 16) =
+          tile * TILE + r < valid ? v[j] : z;
+    }
+    if (PIPE == 1 && fetch_next) load_v(tile + tstride, v);
 
     // hi + lo columns, mask, online softmax (attention.py:21-51 semantics).
-    float x[8];
+    constexpr int kVals = kSub * 4;
+    float x[kVals];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
+    for (int sub = 0; sub < kSub; ++sub) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float v = sacc[sub][j];
-        v += (GMAX <= 4) ? dpp_f32<DPP_ROW_HALF_MIRROR>(v) : dpp_f32<DPP_ROW_MIRROR>(v);
-        const int t = tile * kTile + sub * 16 + kg * 4 + j;
-        x[sub * 4 + j] = t < valid ? v : -INFINITY;
+        float vv = sacc[sub][j];
+        vv += mirror<GMAX>(vv);
+        const int t = tile * TILE + sub * 16 + kg * 4 + j;
+        x[sub * 4 + j] = t < valid ? vv : -INFINITY;
       }
     }
     float tmax = x[0];
 #pragma unroll
-    for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, x[i]);
+    for (int i = 1; i < kVals; ++i) tmax = fmaxf(tmax, x[i]);
     tmax = wave_max_xor(tmax, 16);
     tmax = wave_max_xor(tmax, 32);
     const float m_new = fmaxf(m_run, tmax);
-    float alpha, pr[8];
-    if (m_new == -INFINITY) {
-      alpha = 1.f;
+    // While every score so far is masked, m_new is -inf; subtract 0 instead so
+    // exp2 sees -inf (not NaN): p = 0 and alpha = 0 act on an O and l that are 0.
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    float pr[kVals];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) pr[i] = 0.f;
-    } else {
-      alpha = fast_exp2(m_run - m_new);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(x[i] - m_new);
-    }
+    for (int i = 0; i < kVals; ++i) pr[i] = fast_exp2(x[i] - m_use);
     m_run = m_new;
     float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) psum += pr[i];
+    for (int i = 0; i < kVals; ++i) psum += pr[i];
     l_run = l_run * alpha + psum;
 #pragma unroll
     for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
 
-    // P^T operand: this lane's own 8 probabilities, as bf16 hi or lo.
-    uint32_t p16[8];
+    // P^T operand: this lane's own probabilities, as bf16 hi or lo.
+    uint32_t p16[kVals];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kVals; ++i) {
       const uint32_t hi = f32_to_bf16_bits(pr[i]);
       const uint32_t lo = f32_to_bf16_bits(pr[i] - bf16_bits_to_f32(hi));
-      p16[i] = col_head < 0 ? 0u : (col_lo ? lo : hi);
+      p16[i] = (hi & keep_hi) | (lo & keep_lo);
     }
-    const u32x4 ppk = {pack2(p16[0], p16[1]), pack2(p16[2], p16[3]), pack2(p16[4], p16[5]),
-                       pack2(p16[6], p16[7])};
-    const bf16x8 pop = as_bf16x8(ppk);
 
     // O^T += V^T . P^T, V^T read transposed from LDS.
-    const int i16 = lane & 15;
     const int row1 = 4 * kg + (i16 >> 2);
-    const int row2 = row1 + 16;
+    if constexpr (TILE == 32) {
+      const u32x4 ppk = {pack2(p16[0], p16[1]), pack2(p16[2], p16[3]), pack2(p16[4], p16[5]),
+                         pack2(p16[6], p16[7])};
+      const bf16x8 pop = as_bf16x8(ppk);
+      const int row2 = row1 + 16;
+      constexpr int kBatch = WAVES <= 4 ? kDTiles : kDTiles / 2;  // reads in flight
 #pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) {
-      const int c = dt * 2 + ((i16 & 3) >> 1);
-      const int off = (i16 & 1) * 8;
-      const BT_LDS uint16_t* p0 = (const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row1 * kRowBytes +
-                                                          ((c ^ swz(row1, kSlots)) * 16) + off);
-      const BT_LDS uint16_t* p1 = (const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row2 * kRowBytes +
-                                                          ((c ^ swz(row2, kSlots)) * 16) + off);
-      oacc[dt] = mfma16(lds_read_tr_pair(p0, p1), pop, oacc[dt]);
+      for (int d0 = 0; d0 < kDTiles; d0 += kBatch) {
+        bf16x8 vop[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const int c = (d0 + i) * 2 + ((i16 & 3) >> 1);
+          const int off = (i16 & 1) * 8;
+          const BT_LDS uint16_t* p0 = (const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row1 * kRowBytes +
+                                                              ((c ^ swz(row1, kSlots)) * 16) + off);
+          const BT_LDS uint16_t* p1 = (const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row2 * kRowBytes +
+                                                              ((c ^ swz(row2, kSlots)) * 16) + off);
+          vop[i] = lds_read_tr_pair(p0, p1);
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) oacc[d0 + i] = mfma16(vop[i], pop, oacc[d0 + i]);
+      }
+    } else {
+      const u32x2 pop = {pack2(p16[0], p16[1]), pack2(p16[2], p16[3])};
+      u32x2 vop[kDTiles];
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
+        const int c = dt * 2 + ((i16 & 3) >> 1);
+        const int off = (i16 & 1) * 8;
+        const BT_LDS uint16_t* p0 = (const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row1 * kRowBytes +
+                                                            ((c ^ swz(row1, kSlots)) * 16) + off);
+        vop[dt] = lds_read_tr4(p0);
+      }
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] = mfma16k16(vop[dt], pop, oacc[dt]);
     }
   };
 
-  // ---- tile loop: wave w takes local tiles w, w+4, ...; the next tile's loads
-  // are issued as soon as the current tile's registers have been consumed.
-  const int my_tiles = n_tiles > wave ? (n_tiles - wave + kWaves - 1) / kWaves : 0;
-  if (my_tiles > 0) {
-    u32x4 kr[2][kSteps];
-    u32x4 vr[kVLoads];
-    load_k(tile0 + wave, kr);
-    load_v(tile0 + wave, vr);
+  // ---- tile loop: wave w takes local tiles w, w+WAVES, ... --------------------
+  if constexpr (PIPE == 1) {
     for (int it = 0; it < my_tiles; ++it)
-      compute(tile0 + wave + it * kWaves, it + 1 < my_tiles, kr, vr);
+      compute(tfirst + it * tstride, it + 1 < my_tiles, kr[0], vr[0]);
+  } else {
+    for (int it = 0; it < my_tiles; it += 2) {
+      const int ta = tfirst + it * tstride;
+      compute(ta, false, kr[0], vr[0]);
+      if (it + 2 < my_tiles) {
+        load_k(ta + 2 * tstride, kr[0]);
+        load_v(ta + 2 * tstride, vr[0]);
+      }
+      if (it + 1 >= my_tiles) break;
+      compute(ta + tstride, false, kr[PIPE - 1], vr[PIPE - 1]);
+      if (it + 3 < my_tiles) {
+        load_k(ta + 3 * tstride, kr[PIPE - 1]);
+        load_v(ta + 3 * tstride, vr[PIPE - 1]);
+      }
+    }
   }
 
   // ---- wave epilogue: full row sums, hi + lo merge ---------------------------
@@ -285,15 +438,15 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_decode_split_kernel(DecodeSpl
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float v = oacc[dt][j];
-      oacc[dt][j] = v + ((GMAX <= 4) ? dpp_f32<DPP_ROW_HALF_MIRROR>(v) : dpp_f32<DPP_ROW_MIRROR>(v));
+      oacc[dt][j] = v + mirror<GMAX>(v);
     }
   }
 
   // ---- cross-wave merge through LDS ----------------------------------------
   __syncthreads();  // every wave is done with its V tile
   float* mo = reinterpret_cast<float*>(smem);              // [wave][GMAX][D]
-  float* mm = mo + kWaves * GMAX * D;                       // [wave][GMAX]
-  float* ml = mm + kWaves * GMAX;                           // [wave][GMAX]
+  float* mm = mo + WAVES * GMAX * D;                        // [wave][GMAX]
+  float* ml = mm + WAVES * GMAX;                            // [wave][GMAX]
   if (col < G && !col_lo) {
     float* dst = mo + (wave * GMAX + col) * D;
 #pragma unroll
@@ -314,11 +467,11 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_decode_split_kernel(DecodeSpl
     const int d = (item % (D / 4)) * 4;
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, mm[w * GMAX + h]);
+    for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, mm[w * GMAX + h]);
     float lsum = 0.f;
     float4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < WAVES; ++w) {
       const float lw = ml[w * GMAX + h];
       if (lw > 0.f) {
         const float sc = fast_exp2(mm[w * GMAX + h] - mx);
@@ -339,16 +492,40 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_decode_split_kernel(DecodeSpl
   }
 }
 
-// LSE combine (attention.py:168-189): one work-group per (head, sequence).
-template <int D>
+namespace {
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+}  // namespace
+
+// LSE combine (attention.py:168-189).  One work-group per (head, sequence,
+// 64-column chunk): 16 split groups x 16 float4 columns.  Each thread fetches
+// the partials and LSEs of its splits in one batch; the max and the sum of
+// weights are reduced from those same LSE values, so the kernel makes one
+// memory round trip before its store (splits past the first 16*kPre take a
+// slower second pass).
+template <int D, bool RAGGED>
 __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(CombineParams p) {
-  __shared__ float wts[kMaxSplitsPerSeq];
-  __shared__ float red[256];
+  constexpr int kPre = 8;  // splits per thread fetched up front (16 groups x 8 = 128)
+  __shared__ float red[4];
   __shared__ float4 accs[256];
+  __shared__ float sums[256];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
+  const int chunk = blockIdx.z;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
   int base, ns;
-  if (p.split_base != nullptr) {
+  if constexpr (RAGGED) {
     base = p.split_base[b];
     ns = p.split_count[b];
   } else {
@@ -356,78 +533,113 @@ __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(CombineParams p
     ns = p.num_split;
   }
   const float* lse = p.lse + (int64_t)h * p.total_splits + base;
+  const int c4 = t & 15;   // float4 column inside the 64-column chunk
+  const int sg = t >> 4;   // split group
+  const float* part = p.part + ((int64_t)h * p.total_splits + base) * D + chunk * 64 + c4 * 4;
 
-  float mx = -INFINITY;
-  for (int i = threadIdx.x; i < ns; i += 256) mx = fmaxf(mx, lse[i]);
-  red[threadIdx.x] = mx;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
-    __syncthreads();
+  float4 pv[kPre];
+  float pl[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int s = sg + 16 * i;
+    pl[i] = -INFINITY;
+    pv[i] = float4{0.f, 0.f, 0.f, 0.f};
+    if (s < ns) {
+      pv[i] = *reinterpret_cast<const float4*>(part + (int64_t)s * D);
+      pl[i] = lse[s];
+    }
   }
-  mx = red[0];
+  float mx = pl[0];
+#pragma unroll
+  for (int i = 1; i < kPre; ++i) mx = fmaxf(mx, pl[i]);
+  for (int s = sg + 16 * kPre; s < ns; s += 16) mx = fmaxf(mx, lse[s]);
+  mx = wave_max(mx);
+  if ((t & 63) == 0) red[wave] = mx;
   __syncthreads();
-  float sum = 0.f;
-  for (int i = threadIdx.x; i < ns; i += 256) {
-    const float v = lse[i];
-    const float e = v == -INFINITY ? 0.f : fast_exp2(v - mx);
-    wts[i] = e;
-    sum += e;
-  }
-  red[threadIdx.x] = sum;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-    __syncthreads();
-  }
-  sum = red[0];
-  const float inv = sum > 0.f ? 1.f / sum : 0.f;
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // Empty splits have lse = -inf: weight 0, and their (never written) partial is skipped.
+  const float m_use = mx == -INFINITY ? 0.f : mx;
 
-  // out[d] = sum_s w_s part_s[d] / sum: 4 split groups x (D/4) float4 columns.
-  constexpr int kCols = D / 4;
-  const int grp = threadIdx.x / kCols;
-  const int cidx = threadIdx.x % kCols;
-  constexpr int kGroups = 256 / kCols;
   float4 acc = {0.f, 0.f, 0.f, 0.f};
-  const float* part = p.part + ((int64_t)h * p.total_splits + base) * D + cidx * 4;
-  for (int s = grp; s < ns; s += kGroups) {
-    const float w = wts[s];
-    if (w != 0.f) {
+  float wsum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    if (pl[i] != -INFINITY) {
+      const float w = fast_exp2(pl[i] - m_use);
+      wsum += w;
+      acc.x += w * pv[i].x; acc.y += w * pv[i].y; acc.z += w * pv[i].z; acc.w += w * pv[i].w;
+    }
+  }
+  for (int s = sg + 16 * kPre; s < ns; s += 16) {
+    const float l = lse[s];
+    if (l != -INFINITY) {
+      const float w = fast_exp2(l - m_use);
+      wsum += w;
       const float4 v = *reinterpret_cast<const float4*>(part + (int64_t)s * D);
       acc.x += w * v.x; acc.y += w * v.y; acc.z += w * v.z; acc.w += w * v.w;
     }
   }
-  if (kGroups > 1) {
-    accs[threadIdx.x] = acc;
-    __syncthreads();
-    if (grp == 0) {
-      for (int g2 = 1; g2 < kGroups; ++g2) {
-        const float4 o = accs[g2 * kCols + cidx];
-        acc.x += o.x; acc.y += o.y; acc.z += o.z; acc.w += o.w;
-      }
+  accs[t] = acc;
+  sums[t] = wsum;  // every float4 column sees the same splits; column 0 is counted
+  __syncthreads();
+  if (t < 16) {
+    float4 r = accs[t];
+    float tot = sums[0];
+#pragma unroll
+    for (int g = 1; g < 16; ++g) {
+      const float4 o = accs[g * 16 + t];
+      r.x += o.x; r.y += o.y; r.z += o.z; r.w += o.w;
+      tot += sums[g * 16];
     }
-  }
-  if (grp == 0) {
-    acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
-    const int64_t orow = (int64_t)b * p.out_stride_seq + (int64_t)h * D + cidx * 4;
+    const float inv = tot > 0.f ? 1.f / tot : 0.f;
+    r.x *= inv; r.y *= inv; r.z *= inv; r.w *= inv;
+    const int64_t orow = (int64_t)b * p.out_stride_seq + (int64_t)h * D + chunk * 64 + t * 4;
     if (p.out_bf16) {
       uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + orow;
-      const u32x2 pk = {pack2(f32_to_bf16_bits(acc.x), f32_to_bf16_bits(acc.y)),
-                        pack2(f32_to_bf16_bits(acc.z), f32_to_bf16_bits(acc.w))};
+      const u32x2 pk = {pack2(f32_to_bf16_bits(r.x), f32_to_bf16_bits(r.y)),
+                        pack2(f32_to_bf16_bits(r.z), f32_to_bf16_bits(r.w))};
       *reinterpret_cast<u32x2*>(o) = pk;
     } else {
-      *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow) = acc;
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow) = r;
     }
   }
 }
 
-}  // namespace
+// Production configuration of the split kernel.
+#ifndef BT_DECODE_WAVES
+#define BT_DECODE_WAVES 8
+#endif
+#ifndef BT_DECODE_PIPE
+#define BT_DECODE_PIPE 1
+#endif
 
-template <int GMAX, int D>
+template <int GMAX, int D, int MODE, bool QBF16>
 static hipError_t launch_split_t(const DecodeSplitParams& p, int grid_x, int batch, hipStream_t stream) {
   dim3 grid(grid_x, p.kv_heads, batch);
-  hipLaunchKernelGGL((gqa_decode_split_kernel<GMAX, D>), grid, dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(
+      (gqa_decode_split_kernel<GMAX, D, BT_DECODE_WAVES, BT_DECODE_TILE, BT_DECODE_PIPE, MODE, QBF16>),
+      grid, dim3(BT_DECODE_WAVES * 64), 0, stream, p);
   return hipGetLastError();
+}
+
+template <int GMAX, int D>
+static hipError_t launch_split_mode(const DecodeSplitParams& p, int grid_x, int batch, hipStream_t stream) {
+  const int mode = decode_mode(p.work != nullptr, p.pos != nullptr, p.seq_len != nullptr,
+                               p.seq_offset != nullptr, batch);
+  if (mode < 0) return hipErrorInvalidValue;
+#define BT_SPLIT_CASE(M)                                                                      \
+  case M:                                                                                     \
+    return p.q_bf16 ? launch_split_t<GMAX, D, M, true>(p, grid_x, batch, stream)              \
+                    : launch_split_t<GMAX, D, M, false>(p, grid_x, batch, stream);
+  switch (mode) {
+    BT_SPLIT_CASE(kModeLen)
+    BT_SPLIT_CASE(kModePos)
+    BT_SPLIT_CASE(kModePosBatch)
+    BT_SPLIT_CASE(kModeRagged)
+    BT_SPLIT_CASE(kModeLenBatch)
+    default: return hipErrorInvalidValue;
+  }
+#undef BT_SPLIT_CASE
 }
 
 hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int grid_x, int batch,
@@ -435,20 +647,28 @@ hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int gri
   const int G = p.heads / p.kv_heads;
   const bool small = G <= 4;
   switch (head_dim) {
-    case 64: return small ? launch_split_t<4, 64>(p, grid_x, batch, stream) : launch_split_t<8, 64>(p, grid_x, batch, stream);
-    case 128: return small ? launch_split_t<4, 128>(p, grid_x, batch, stream) : launch_split_t<8, 128>(p, grid_x, batch, stream);
-    case 256: return small ? launch_split_t<4, 256>(p, grid_x, batch, stream) : launch_split_t<8, 256>(p, grid_x, batch, stream);
+    case 64: return small ? launch_split_mode<4, 64>(p, grid_x, batch, stream) : launch_split_mode<8, 64>(p, grid_x, batch, stream);
+    case 128: return small ? launch_split_mode<4, 128>(p, grid_x, batch, stream) : launch_split_mode<8, 128>(p, grid_x, batch, stream);
+    case 256: return small ? launch_split_mode<4, 256>(p, grid_x, batch, stream) : launch_split_mode<8, 256>(p, grid_x, batch, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
+template <int D>
+static void launch_combine_t(const CombineParams& p, dim3 grid, hipStream_t stream) {
+  if (p.split_base != nullptr)
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, true>), grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, false>), grid, dim3(256), 0, stream, p);
+}
+
 hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads, int batch,
                                  hipStream_t stream) {
-  dim3 grid(heads, batch);
+  dim3 grid(heads, batch, head_dim / 64);
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL(gqa_decode_combine_kernel<64>, grid, dim3(256), 0, stream, p); break;
-    case 128: hipLaunchKernelGGL(gqa_decode_combine_kernel<128>, grid, dim3(256), 0, stream, p); break;
-    case 256: hipLaunchKernelGGL(gqa_decode_combine_kernel<256>, grid, dim3(256), 0, stream, p); break;
+    case 64: launch_combine_t<64>(p, grid, stream); break;
+    case 128: launch_combine_t<128>(p, grid, stream); break;
+    case 256: launch_combine_t<256>(p, grid, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

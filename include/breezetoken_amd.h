@@ -55,13 +55,22 @@ int64_t bt_decode_workspace_bytes(int32_t heads, int32_t head_dim, int32_t total
  * `num_cus` compute units (the reference hard-codes 16, backends.py:526,550). */
 int32_t bt_decode_pick_splits(int32_t kv_heads, int32_t ctx_len, int32_t num_cus);
 
+/* Tokens per tile.  The split pass deals tiles to splits round-robin: tile t
+ * (tokens [t*T, (t+1)*T)) belongs to split t % num_split.  The reference gives
+ * each split a contiguous range instead (attention.py:106-112); the combined
+ * output is the same, only the per-split partials differ. */
+int32_t bt_decode_tile_tokens(void);
+
 /* Split-KV pass: the first kernel of gqa_decode / gqa_decode_fixed
  * (breezetoken/kernels/cuda/attention.py:88-166 and 249-326).  The valid length
  * of sequence b is pos[b] + 1 when pos != NULL (the device position tensor of
  * the graph path, attention.py:296-301), else seq_len[b] when seq_len != NULL,
- * else `seqlen`.  seq_offset (nullable) gives each sequence's first slot.
- * Writes lse/part rows [b*num_split, (b+1)*num_split) of every head;
- * total_splits = batch*num_split. */
+ * else `seqlen`.  When pos != NULL, `seqlen` must be the cache capacity in
+ * slots (>= 1): no slot at or past it is read and pos[b] + 1 is clamped to it.
+ * seq_offset gives each sequence's first slot; it is required when batch > 1
+ * (with pos or seq_len) and must be NULL otherwise; pos and seq_len are
+ * exclusive.  Writes lse/part rows [b*num_split, (b+1)*num_split) of every
+ * head; total_splits = batch*num_split. */
 int bt_gqa_decode_split(const void* q, int32_t q_dtype, int64_t q_stride_seq,
                         const void* k, const void* v, int64_t kv_stride_tok,
                         int64_t kv_stride_head, const int64_t* seq_offset, const int32_t* pos,

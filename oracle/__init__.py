@@ -20,7 +20,10 @@ What each function restates, and what pins it (see ``tests/test_oracle.py``):
   partition, per-split log2-domain LSE + normalised partial, empty-split rule
   and LSE combine of ``gqa_decode`` (breezetoken/kernels/cuda/attention.py:
   104-112, 153-166, 168-189).  Pinned by: combine(split) == unsplit for every
-  split count, empty split -> (-inf, 0), closed-form LSE.
+  split count and both partitions, empty split -> (-inf, 0), closed-form LSE.
+* ``round_robin_partition`` -- the MI355X kernel's dealing of tiles to splits
+  (tile t -> split t % NS), which replaces attention.py:106-112.  Pinned by:
+  every token in exactly one split, combine == unsplit.
 * ``fixed_decode`` -- the fixed-capacity/device-position contract of
   ``gqa_decode_fixed`` (attention.py:296-301, valid = pos + 1) on top of
   ``torch_attention``.  Pinned by: equality with ``torch_attention`` on the

@@ -177,13 +177,24 @@ def split_partition(seqlen: int, num_split: int, block_n: int = 32) -> list[tupl
     return out
 
 
-def split_decode(q, k, v, scale: float, num_split: int, block_n: int = 32):
+def round_robin_partition(seqlen: int, num_split: int, block_n: int) -> list[np.ndarray]:
+    """Token indices of every split when tile t (tokens [t*block_n, (t+1)*block_n))
+    goes to split t % num_split -- the MI355X kernel's dealing, which replaces the
+    contiguous ranges of attention.py:106-112 (the combined output is the same)."""
+    idx = np.arange(seqlen)
+    tile = idx // block_n
+    return [idx[tile % num_split == s] for s in range(num_split)]
+
+
+def split_decode(q, k, v, scale: float, num_split: int, block_n: int = 32,
+                 partition: str = "contiguous"):
     """Per-split (Lse, Part) of ``gqa_decode``'s split kernel (attention.py:114-166), float64.
 
     Returns ``lse`` (H, NS) in the log2 domain, ``lse = log2(l) + m * scale *
     log2e`` with ``l = sum exp2((s - m) * scale * log2e)``, and ``part`` (H, NS,
     D) = the split's normalised output.  An empty split has lse = -inf and a
-    zero partial (attention.py:153-160).
+    zero partial (attention.py:153-160).  ``partition`` is ``"contiguous"`` (the
+    reference, ``split_partition``) or ``"round_robin"`` (``round_robin_partition``).
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -194,16 +205,22 @@ def split_decode(q, k, v, scale: float, num_split: int, block_n: int = 32):
     c = scale * LOG2E
     lse = np.full((heads, num_split), -np.inf)
     part = np.zeros((heads, num_split, dim))
-    for s, (b, e) in enumerate(split_partition(k.shape[0], num_split, block_n)):
-        if e <= b:
+    if partition == "contiguous":
+        rows = [np.arange(b, e) for b, e in split_partition(k.shape[0], num_split, block_n)]
+    elif partition == "round_robin":
+        rows = round_robin_partition(k.shape[0], num_split, block_n)
+    else:
+        raise ValueError(f"unknown partition {partition!r}")
+    for s, r in enumerate(rows):
+        if r.size == 0:
             continue
         for h in range(heads):
             g = h // group
-            x = (k[b:e, g, :] @ q[h]) * c  # log2-domain scores
+            x = (k[r, g, :] @ q[h]) * c  # log2-domain scores
             m = x.max()
             p = np.exp2(x - m)
             l_sum = p.sum()
-            part[h, s] = (p @ v[b:e, g, :]) / l_sum
+            part[h, s] = (p @ v[r, g, :]) / l_sum
             lse[h, s] = math.log2(l_sum) + m
     return lse, part
 

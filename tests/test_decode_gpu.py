@@ -120,10 +120,12 @@ def test_deterministic(hip_backend):
 @pytest.mark.parametrize("seq,ns", [(1000, 1), (1000, 3), (1000, 16), (1000, 40), (100, 16), (4096, 128)])
 def test_split_partials_match_oracle(hip_backend, seq, ns):
     """Per-split LSE (log2 domain) and normalised partials against the restated split
-    kernel (attention.py:114-166); empty splits report lse = -inf."""
+    kernel (attention.py:114-166) with the kernel's round-robin dealing of tiles;
+    empty splits report lse = -inf."""
     case = wl.decode_inputs(23, 8, 2, 256, seq, seq)
     lse_ref, part_ref = orc.split_decode(case.q.float().numpy(), case.k.float().numpy(),
-                                         case.v.float().numpy(), case.scale, ns)
+                                         case.v.float().numpy(), case.scale, ns,
+                                         block_n=hip_backend.tile_tokens, partition="round_robin")
     q, k, v = _dev(case.q.float(), case.k, case.v)
     lse, part = hip_backend.decode_partials(q, k, v, case.scale, ns)
     lse, part = lse.cpu().numpy(), part.cpu().numpy()
@@ -135,6 +137,36 @@ def test_split_partials_match_oracle(hip_backend, seq, ns):
     # the device combine of device partials equals the oracle combine
     out = hip_backend.combine(torch.from_numpy(lse).cuda(), torch.from_numpy(part).cuda())
     assert_close(out, orc.combine_lse(lse_ref, part_ref))
+
+
+@pytest.mark.parametrize("valid,ns", [(1, 128), (33, 128), (1000, 128), (4096, 128), (5000, 7)])
+def test_split_partials_position_path(hip_backend, valid, ns):
+    """The device-position path (first tile fetched before the position is read) on a
+    cache whose slots past the position hold NaN/inf."""
+    cap = 8192
+    case = wl.decode_inputs(27, 8, 2, 256, cap, valid)
+    kd, vd = case.k.clone(), case.v.clone()
+    kd[valid:] = float("nan")
+    vd[valid:] = float("inf")
+    lse_ref, part_ref = orc.split_decode(case.q.float().numpy(), case.k[:valid].float().numpy(),
+                                         case.v[:valid].float().numpy(), case.scale, ns,
+                                         block_n=hip_backend.tile_tokens, partition="round_robin")
+    q, k, v = _dev(case.q.float(), kd, vd)
+    pos = torch.tensor([valid - 1], dtype=torch.int32, device="cuda")
+    lse, part = hip_backend.decode_partials(q, k, v, case.scale, ns, pos=pos)
+    lse, part = lse.cpu().numpy(), part.cpu().numpy()
+    empty = np.isneginf(lse_ref)
+    assert np.array_equal(np.isneginf(lse), empty)
+    assert np.abs(lse[~empty] - lse_ref[~empty]).max() < 1e-3
+    assert np.abs(part[~empty] - part_ref[~empty]).max() < ATOL
+
+
+def test_position_past_capacity_is_clamped(hip_backend):
+    case = wl.decode_inputs(28, 8, 2, 256, 512, 512)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    pos = torch.tensor([10_000], dtype=torch.int32, device="cuda")
+    out = hip_backend.attention_fixed(q, k, v, pos, case.scale)
+    assert_close(out, orc.torch_attention(case.q.float(), case.k.float(), case.v.float(), case.scale))
 
 
 def test_combine_of_oracle_partials(hip_backend):

@@ -151,19 +151,30 @@ def test_split_partition_covers_context(seq, tiles_per, ns):
     assert tiles == [base + (1 if s < extra else 0) for s in range(ns)]
 
 
+@pytest.mark.parametrize("seq,ns,block", [(1, 4, 32), (100, 3, 16), (1000, 16, 32), (1000, 7, 16), (33, 2, 32)])
+def test_round_robin_partition_covers_every_token_once(seq, ns, block):
+    parts = orc.round_robin_partition(seq, ns, block)
+    allidx = np.sort(np.concatenate(parts))
+    assert np.array_equal(allidx, np.arange(seq))
+    for s, r in enumerate(parts):
+        assert np.all((r // block) % ns == s)
+
+
+@pytest.mark.parametrize("partition", ["contiguous", "round_robin"])
 @pytest.mark.parametrize("seq", [1, 17, 100, 128, 1000])
 @pytest.mark.parametrize("ns", [1, 2, 3, 5, 16, 64])
-def test_combine_of_splits_equals_unsplit(seq, ns):
+def test_combine_of_splits_equals_unsplit(seq, ns, partition):
     q, k, v = _decode_inputs(seq, seed=seq * 7 + ns)
-    lse, part = orc.split_decode(q.numpy(), k.numpy(), v.numpy(), SCALE, ns)
+    lse, part = orc.split_decode(q.numpy(), k.numpy(), v.numpy(), SCALE, ns, partition=partition)
     out = orc.combine_lse(lse, part)
     ref = orc.brute_force_decode_f64(q.numpy(), k.numpy(), v.numpy(), SCALE)
     assert orc.compare(out, ref)[0] < 1e-12
 
 
-def test_empty_split_rule():
+@pytest.mark.parametrize("partition", ["contiguous", "round_robin"])
+def test_empty_split_rule(partition):
     q, k, v = _decode_inputs(40, seed=12)  # 2 tiles, 16 splits -> 14 empty
-    lse, part = orc.split_decode(q.numpy(), k.numpy(), v.numpy(), SCALE, 16)
+    lse, part = orc.split_decode(q.numpy(), k.numpy(), v.numpy(), SCALE, 16, partition=partition)
     assert np.isneginf(lse[:, 2:]).all()
     assert np.all(part[:, 2:] == 0)
     assert np.isfinite(lse[:, :2]).all()
