@@ -59,6 +59,7 @@ struct PrefillParams {
   int32_t seqlen;
   int32_t heads;
   int32_t kv_heads;
+  int32_t group;       // heads / kv_heads
   float scale_log2;
   void* out;
   int out_bf16;

@@ -281,6 +281,7 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   p.seqlen = seqlen;
   p.heads = heads;
   p.kv_heads = kv_heads;
+  p.group = heads / kv_heads;
   p.scale_log2 = (float)((double)scale * kLog2e);
   p.out = out;
   p.out_bf16 = out_dtype == BT_DTYPE_BF16;

@@ -1,0 +1,121 @@
+"""GPU parity of the causal GQA prefill kernel against the CPU oracle.
+
+The f32-output mode is held to the decode gate (max-abs <= 2e-3, cosine >=
+0.99999) against the restated causal SDPA (prefill.py:56-68) in f32 on the same
+bf16 inputs.  The bf16-output mode is compared with that reference rounded to
+bf16: one bf16 rounding of |o| ~ 2-4 alone is up to 2^-8 * 4 = 1.6e-2, so the
+bound there is 2e-3 plus one bf16 half-ulp of the reference value.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from breezetoken_amd import workloads as wl
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+COS = 0.99999
+
+
+def _close(got, ref, atol=ATOL, cos_min=COS):
+    g = got.detach().float().cpu().numpy()
+    r = ref.detach().float().cpu().numpy() if isinstance(ref, torch.Tensor) else np.asarray(ref)
+    assert np.isfinite(g).all(), "non-finite output"
+    err, cos = orc.compare(g, r)
+    assert err <= atol and cos >= cos_min, f"max-abs {err:.3e}, cosine {cos:.8f}"
+
+
+def _inputs(steps, heads=8, kv=2, dim=256, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(steps, heads, dim, generator=g).to(torch.bfloat16)
+    k = torch.randn(steps, kv, dim, generator=g).to(torch.bfloat16)
+    v = torch.randn(steps, kv, dim, generator=g).to(torch.bfloat16)
+    return q, k, v, dim**-0.5
+
+
+@pytest.mark.parametrize("steps", [128, 512, 2048])
+def test_c4_prefill_f32_output(hip_backend, steps):
+    q, k, v, scale = wl.c4_inputs(steps)
+    print(f"[c4] S={steps}", flush=True)
+    ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale)
+    assert out.shape == (steps, 8, 256) and out.dtype == torch.float32
+    _close(out, ref)
+
+
+def test_c4_prefill_8192_sampled_rows(hip_backend):
+    """S = 8192: every sampled row i must equal decode attention over keys 0..i."""
+    q, k, v, scale = wl.c4_inputs(8192)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu()
+    rows = [0, 1, 31, 32, 63, 64, 1000, 4095, 4096, 8000, 8190, 8191]
+    for i in rows:
+        ref = orc.torch_attention(q[i].float(), k[: i + 1].float(), v[: i + 1].float(), scale)
+        _close(out[i], ref)
+
+
+@pytest.mark.parametrize("steps", [128, 2048])
+def test_c4_prefill_bf16_output(hip_backend, steps):
+    q, k, v, scale = wl.c4_inputs(steps)
+    ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, out_dtype=torch.bfloat16)
+    assert out.dtype == torch.bfloat16
+    g = out.float().cpu()
+    half_ulp = ref.abs().clamp_min(2.0**-126).log2().floor().exp2() * 2.0**-8
+    assert ((g - ref).abs() <= ATOL + half_ulp).all()
+    _close(g, ref.to(torch.bfloat16).float(), atol=4e-3 + 2.0**-7)
+
+
+@pytest.mark.parametrize("steps", [1, 2, 7, 33, 65, 100, 257, 1000])
+def test_ragged_prompt_lengths(hip_backend, steps):
+    q, k, v, scale = _inputs(steps, seed=steps)
+    ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    _close(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale), ref)
+
+
+@pytest.mark.parametrize("heads,kv,dim", [(8, 2, 128), (4, 4, 256), (8, 4, 256), (16, 2, 256), (8, 8, 128),
+                                          (6, 2, 256), (12, 2, 128)])
+def test_other_group_sizes(hip_backend, heads, kv, dim):
+    q, k, v, scale = _inputs(300, heads, kv, dim, seed=heads * 100 + kv)
+    ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    _close(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale), ref)
+
+
+def test_sdpa_shaped_shim(hip_backend):
+    """The (1, H, S, D) call of prefill.py:60-68, including transposed views."""
+    q, k, v, scale = _inputs(200)
+    qq = q.cuda().transpose(0, 1).unsqueeze(0)
+    kk = k.cuda().transpose(0, 1).unsqueeze(0)
+    vv = v.cuda().transpose(0, 1).unsqueeze(0)
+    out = hip_backend.sdpa_prefill(qq, kk, vv, scale)
+    assert out.shape == (1, 8, 200, 256)
+    ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    _close(out[0].transpose(0, 1), ref)
+
+
+def test_prefill_rows_match_decode_kernel(hip_backend):
+    """Row i of prefill equals the decode kernel over keys 0..i (test_model.py:92-98's
+    batched == token-wise property, at the attention level)."""
+    q, k, v, scale = _inputs(300, seed=11)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale)
+    kd, vd = k.cuda(), v.cuda()
+    for i in (0, 5, 63, 64, 199, 299):
+        dec = hip_backend.attention(q[i].float().cuda(), kd[: i + 1], vd[: i + 1], scale)
+        _close(out[i], dec, atol=1e-3)
+
+
+def test_prefill_deterministic(hip_backend):
+    q, k, v, scale = _inputs(500, seed=12)
+    a = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).clone()
+    b = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale)
+    assert torch.equal(a, b)
+
+
+def test_prefill_unserved_raises(hip_backend):
+    q, k, v, scale = _inputs(16, dim=64)
+    with pytest.raises(RuntimeError):
+        hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale)
