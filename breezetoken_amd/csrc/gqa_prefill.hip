@@ -21,8 +21,11 @@
 //  * online softmax in the log2 domain with lazy rescaling: the reference
 //    maximum only moves (and O^T is only rescaled) when a score exceeds it by
 //    more than 2^8, so most key blocks skip the 128-register rescale;
-//  * K/V tiles are double-buffered through registers: the next block's global
-//    loads are in flight while the current block is multiplied;
+//  * software pipeline over 64-key blocks: iteration i stages K_{i+1} and V_i
+//    into LDS and fetches K_{i+2} / V_{i+1} from HBM while multiplying
+//    S_i = K_i . Q^T, then runs the softmax of S_i next to O += V_{i-1} . P_{i-1},
+//    so matrix-core work always has independent VALU/LDS work beside it; every
+//    buffer is rewritten only after the barrier that ends its last reader;
 //  * heavy (late) query blocks are launched first to balance the causal work.
 #include "bt_common.h"
 #include "bt_kernels.h"
@@ -117,28 +120,34 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)S * row_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.v + (int64_t)kvh * p.kv_stride_head, (uint32_t)S * row_bytes);
 
-  // Staging: thread t moves chunks id = i * 256 + t (row id / kChunks, chunk id % kChunks).
+  // Staging: at step i thread t moves chunk (t % kChunks) of row i * kRowsPerStep + t / kChunks;
+  // the lane part of every address is computed once, the step part is an
+  // immediate (LDS) or a scalar offset (global).
+  constexpr int kRowsPerStep = kWaves * 64 / kChunks;
+  const uint32_t g_lane = (uint32_t)(t / kChunks) * row_bytes + (t % kChunks) * 16;
+  const int k_lane = (t / kChunks) * kKStride + (t % kChunks) * 16;
+  const int v_lane = (t / kChunks) * kVStride + (t % kChunks) * 16;
   u32x4 kst[kLoads], vst[kLoads];
-  auto load_kv = [&](int kb) {
+  auto load_k = [&](int kb) {
     const uint32_t so = (uint32_t)(kb * kKB) * row_bytes;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int id = i * kWaves * 64 + t;
-      const uint32_t off = (uint32_t)(id / kChunks) * row_bytes + (id % kChunks) * 16;
-      kst[i] = buf_load16(krs, off, so);
-      vst[i] = buf_load16(vrs, off, so);
-    }
+    for (int i = 0; i < kLoads; ++i) kst[i] = buf_load16(krs, g_lane, so + (uint32_t)(i * kRowsPerStep) * row_bytes);
   };
-  auto store_kv = [&](int buf) {
-    unsigned char* kb_lds = smem + buf * kBufBytes;
-    unsigned char* vb_lds = kb_lds + kKTile;
+  auto load_v = [&](int kb) {
+    const uint32_t so = (uint32_t)(kb * kKB) * row_bytes;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int id = i * kWaves * 64 + t;
-      const int row = id / kChunks, c = id % kChunks;
-      *reinterpret_cast<u32x4*>(kb_lds + row * kKStride + c * 16) = kst[i];
-      *reinterpret_cast<u32x4*>(vb_lds + row * kVStride + c * 16) = bf16x8_to_f16x8(vst[i]);
-    }
+    for (int i = 0; i < kLoads; ++i) vst[i] = buf_load16(vrs, g_lane, so + (uint32_t)(i * kRowsPerStep) * row_bytes);
+  };
+  auto store_k = [&](int buf) {
+    unsigned char* dst = smem + buf * kBufBytes + k_lane;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) *reinterpret_cast<u32x4*>(dst + i * kRowsPerStep * kKStride) = kst[i];
+  };
+  auto store_v = [&](int buf) {
+    unsigned char* dst = smem + buf * kBufBytes + kKTile + v_lane;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i)
+      *reinterpret_cast<u32x4*>(dst + i * kRowsPerStep * kVStride) = bf16x8_to_f16x8(vst[i]);
   };
 
   const int qcol = lane & 31;       // this lane's query column
@@ -149,8 +158,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
 
   const int passes = (G + kWaves - 1) / kWaves;
   for (int pass = 0; pass < passes; ++pass) {
-    const int head = kvh * G + pass * kWaves + wave % GW;
-    const bool wave_active = wave < GW * (kWaves / GW) && pass * kWaves + wave % GW < G && q0 < S;
+    const int head_local = pass * kWaves + wave % GW;
+    // Waves past the group (or past the prompt) run the same instruction stream
+    // on clamped indices and store nothing; their keys beyond their queries are
+    // masked like any causal key, so no branch is needed inside the key loop.
+    const bool wave_active = wave < GW * (kWaves / GW) && head_local < G && q0 < S;
+    const int head = kvh * G + min(head_local, G - 1);
 
     // ---- Q^T operand in registers: lane holds Q[q0 + qcol][d = st*16 + kgrp*8 .. +8]
     u32x4 qop[kSteps];
@@ -169,89 +182,117 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     float m_ref = -INFINITY;  // reference max (log2 domain) of this lane's column
     float l_run = 0.f;        // partial row sum over this lane's keys
     const int my_q = q0 + qcol;
-    const int wave_kend = min(S, q0 + kQB);  // keys this wave needs: [0, wave_kend)
+    uint32_t pk[2][8];        // P of the latest key block (fp16 pairs)
 
-    load_kv(0);
-    store_kv(0);
-    __syncthreads();
-
-    for (int kb = 0; kb < nkb; ++kb) {
-      const int buf = kb & 1;
-      if (kb + 1 < nkb) load_kv(kb + 1);
-      const unsigned char* kb_lds = smem + buf * kBufBytes;
-      const unsigned char* vb_lds = kb_lds + kKTile;
-      const int key0 = kb * kKB;
-
-      if (wave_active && key0 < wave_kend) {
-        // S^T (64 keys x 32 queries) = K . Q^T
-        floatx16 sacc[2];
+    // S^T (64 keys x 32 queries) = K . Q^T from K buffer `buf`.
+    auto qk = [&](int buf, floatx16 (&sacc)[2]) {
+      const unsigned char* krow = smem + buf * kBufBytes + qcol * kKStride + kgrp * 16;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int j = 0; j < 16; ++j) sacc[mt][j] = 0.f;
-        const unsigned char* krow = kb_lds + qcol * kKStride + kgrp * 16;
+        for (int j = 0; j < 16; ++j) sacc[mt][j] = 0.f;
 #pragma unroll
-        for (int st = 0; st < kSteps; ++st) {
+      for (int st = 0; st < kSteps; ++st) {
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-            const u32x4 a = *reinterpret_cast<const u32x4*>(krow + mt * 32 * kKStride + st * 32);
-            sacc[mt] = mfma32(as_bf16x8(a), as_bf16x8(qop[st]), sacc[mt]);
-          }
-        }
-
-        // scale, causal mask, tile max over this lane's 32 keys and its partner lane's
-        const bool diag = key0 + kKB - 1 > q0;  // some key of the block may be past some query
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int key = key0 + mt * 32 + (j >> 2) * 8 + kgrp * 4 + (j & 3);
-            float v = sacc[mt][j] * c_log2;
-            if (diag) v = key <= my_q ? v : -INFINITY;
-            sacc[mt][j] = v;
-            tmax = fmaxf(tmax, v);
-          }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        // lazy reference max: move it only when a score exceeds it by > kLazy
-        if (tmax > m_ref + kLazy) {
-          const float alpha = fast_exp2(m_ref - tmax);  // 0 when m_ref is -inf
-          l_run *= alpha;
-#pragma unroll
-          for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
-          m_ref = tmax;
-        }
-        const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
-        uint32_t pk[2][8];
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int j = 0; j < 16; j += 2) {
-            const float p0 = fast_exp2(sacc[mt][j] - m_use);
-            const float p1 = fast_exp2(sacc[mt][j + 1] - m_use);
-            l_run += p0 + p1;
-            pk[mt][j / 2] = pack_f16_rne(p0, p1);
-          }
-
-        // O^T (D x 32) += V^T (D x 64 keys) . P^T (64 keys x 32)
-        // transposed reads: lane's row (kgrp*4 + i16/4) and columns (sub16*16 + (i16%4)*4)
-        const unsigned char* vlane = vb_lds + (kgrp * 4 + (i16 >> 2)) * kVStride + (sub16 * 16 + (i16 & 3) * 4) * 2;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const int mt = ks >> 1, half = ks & 1;
-          const u32x4 pop = {pk[mt][half * 4 + 0], pk[mt][half * 4 + 1], pk[mt][half * 4 + 2], pk[mt][half * 4 + 3]};
-#pragma unroll
-          for (int dt = 0; dt < kDTiles; ++dt) {
-            const unsigned char* pa = vlane + ks * 16 * kVStride + dt * 64;
-            const bf16x8 vt = lds_read_tr_pair((const BT_LDS uint16_t*)(const BT_LDS unsigned char*)pa,
-                                               (const BT_LDS uint16_t*)(const BT_LDS unsigned char*)(pa + 8 * kVStride));
-            oacc[dt] = mfma32_f16(__builtin_bit_cast(u32x4, vt), pop, oacc[dt]);
-          }
+        for (int mt = 0; mt < 2; ++mt) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(krow + mt * 32 * kKStride + st * 32);
+          sacc[mt] = mfma32(as_bf16x8(a), as_bf16x8(qop[st]), sacc[mt]);
         }
       }
-      if (kb + 1 < nkb) store_kv(buf ^ 1);
+    };
+    // O^T += V^T . P^T over the 64 keys held in V buffer `buf`.
+    auto pv = [&](int buf) {
+      const unsigned char* vlane = smem + buf * kBufBytes + kKTile + (kgrp * 4 + (i16 >> 2)) * kVStride +
+                                   (sub16 * 16 + (i16 & 3) * 4) * 2;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int mt = ks >> 1, half = ks & 1;
+        const u32x4 pop = {pk[mt][half * 4 + 0], pk[mt][half * 4 + 1], pk[mt][half * 4 + 2], pk[mt][half * 4 + 3]};
+#pragma unroll
+        for (int dt = 0; dt < kDTiles; ++dt) {
+          const unsigned char* pa = vlane + ks * 16 * kVStride + dt * 64;
+          const bf16x8 vt = lds_read_tr_pair((const BT_LDS uint16_t*)(const BT_LDS unsigned char*)pa,
+                                             (const BT_LDS uint16_t*)(const BT_LDS unsigned char*)(pa + 8 * kVStride));
+          oacc[dt] = mfma32_f16(__builtin_bit_cast(u32x4, vt), pop, oacc[dt]);
+        }
+      }
+    };
+    // Scale, causal mask and online softmax of block kb; fills pk and returns
+    // the factor the accumulated O must be scaled by (1 unless the max moved).
+    auto softmax = [&](int kb, floatx16 (&sacc)[2]) -> float {
+      const int key0 = kb * kKB;
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = key0 + mt * 32 + (j >> 2) * 8 + kgrp * 4 + (j & 3);
+          const float v = key <= my_q ? sacc[mt][j] * c_log2 : -INFINITY;
+          sacc[mt][j] = v;
+          tmax = fmaxf(tmax, v);
+        }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      // lazy reference max: move it only when a score exceeds it by > kLazy
+      const bool move = tmax > m_ref + kLazy;
+      const float m_new = move ? tmax : m_ref;
+      const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
+      m_ref = m_new;
+      const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+      float psum = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+          const float p0 = fast_exp2(sacc[mt][j] - m_use);
+          const float p1 = fast_exp2(sacc[mt][j + 1] - m_use);
+          psum += p0 + p1;
+          pk[mt][j / 2] = pack_f16_rne(p0, p1);
+        }
+      l_run = l_run * alpha + psum;
+      return alpha;
+    };
+    auto rescale = [&](float alpha) {
+      if (alpha != 1.f) {
+#pragma unroll
+        for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
+      }
+    };
+
+    // Prologue: K_0 in LDS, K_1 and V_0 in flight.
+    load_k(0);
+    load_v(0);
+    store_k(0);
+    if (1 < nkb) load_k(1);
+    __syncthreads();
+
+    // Block 0: stage K_1 / V_0, S_0, softmax -> P_0.
+    {
+      if (1 < nkb) store_k(1);
+      store_v(0);
+      if (2 < nkb) load_k(2);
+      if (1 < nkb) load_v(1);
+      floatx16 sacc[2];
+      qk(0, sacc);
+      rescale(softmax(0, sacc));
       __syncthreads();
     }
+    // Block kb: stage K_{kb+1} and V_kb, fetch K_{kb+2} and V_{kb+1},
+    // S_kb = K_kb . Q^T, O += V_{kb-1} . P_{kb-1}, softmax(S_kb) -> P_kb.
+    // Buffers written here (K (kb+1)%2, V kb%2) were last read before the
+    // previous barrier, so one barrier per block suffices.
+    for (int kb = 1; kb < nkb; ++kb) {
+      const int buf = kb & 1;
+      if (kb + 1 < nkb) store_k(buf ^ 1);
+      store_v(buf);
+      if (kb + 2 < nkb) load_k(kb + 2);
+      if (kb + 1 < nkb) load_v(kb + 1);
+      floatx16 sacc[2];
+      qk(buf, sacc);
+      pv(buf ^ 1);
+      rescale(softmax(kb, sacc));
+      __syncthreads();
+    }
+    pv((nkb - 1) & 1);
 
     // ---- epilogue: full row sums, normalise, store ---------------------------
     l_run += __shfl_xor(l_run, 32, 64);
@@ -275,6 +316,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
         }
       }
     }
+    __syncthreads();  // the next pass restages buffer 0
   }
 }
 
