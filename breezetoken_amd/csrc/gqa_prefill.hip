@@ -35,6 +35,9 @@ namespace bt {
 namespace {
 
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+
 
 constexpr int kQB = 32;      // query positions per wave
 constexpr int kKB = 64;      // keys per step
@@ -58,10 +61,11 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
 __device__ __forceinline__ uint32_t pack_f16_rtz(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
-// Two floats -> packed fp16 pair, round to nearest even.
+// Two floats -> packed fp16 pair, round to nearest even (one v_cvt_pk_f16_f32).
 __device__ __forceinline__ uint32_t pack_f16_rne(float a, float b) {
-  const _Float16 x = (_Float16)a, y = (_Float16)b;
-  return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+  uint32_t r;
+  asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
 }
 
 __device__ __forceinline__ u32x4 bf16x8_to_f16x8(const u32x4& v) {
@@ -217,34 +221,40 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
         }
       }
     };
-    // Scale, causal mask and online softmax of block kb; fills pk and returns
-    // the factor the accumulated O must be scaled by (1 unless the max moved).
-    auto softmax = [&](int kb, floatx16 (&sacc)[2]) -> float {
+    // Causal mask of block kb (only blocks reaching past q0 need it).
+    auto mask = [&](int kb, floatx16(&sacc)[2]) {
       const int key0 = kb * kKB;
-      float tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int key = key0 + mt * 32 + (j >> 2) * 8 + kgrp * 4 + (j & 3);
-          const float v = key <= my_q ? sacc[mt][j] * c_log2 : -INFINITY;
-          sacc[mt][j] = v;
-          tmax = fmaxf(tmax, v);
+          sacc[mt][j] = key <= my_q ? sacc[mt][j] : -INFINITY;
         }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    };
+    // Online softmax of one block: fills pk and returns the factor the
+    // accumulated O must be scaled by (1 unless the reference max moved).
+    // Scores stay unscaled until exp2(s * c - m).
+    auto softmax = [&](floatx16(&sacc)[2]) -> float {
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) tmax = fmaxf(tmax, sacc[mt][j]);
+      tmax = halves_max(tmax) * c_log2;
       // lazy reference max: move it only when a score exceeds it by > kLazy
       const bool move = tmax > m_ref + kLazy;
       const float m_new = move ? tmax : m_ref;
       const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
       m_ref = m_new;
-      const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+      const float neg_m = m_ref == -INFINITY ? 0.f : -m_ref;
       float psum = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
-          const float p0 = fast_exp2(sacc[mt][j] - m_use);
-          const float p1 = fast_exp2(sacc[mt][j + 1] - m_use);
+          const float p0 = fast_exp2(fmaf(sacc[mt][j], c_log2, neg_m));
+          const float p1 = fast_exp2(fmaf(sacc[mt][j + 1], c_log2, neg_m));
           psum += p0 + p1;
           pk[mt][j / 2] = pack_f16_rne(p0, p1);
         }
@@ -252,28 +262,34 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       return alpha;
     };
     auto rescale = [&](float alpha) {
-      if (alpha != 1.f) {
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max moved by > 2^8
 #pragma unroll
         for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
       }
     };
+    // Blocks whose last key is <= q0 need no causal mask.
+    const int kb_diag = (q0 + 1) / kKB;
+    const int last = nkb - 1;
 
-    // Prologue: K_0 in LDS, K_1 and V_0 in flight.
+    // Prologue: K_0 in LDS, K_1 and V_0 in flight.  Fetches past the last
+    // block re-read the last block (min(., last)) and are never consumed, so
+    // the key loop has no branches around its loads and stores.
     load_k(0);
     load_v(0);
     store_k(0);
-    if (1 < nkb) load_k(1);
+    load_k(min(1, last));
     __syncthreads();
 
     // Block 0: stage K_1 / V_0, S_0, softmax -> P_0.
     {
-      if (1 < nkb) store_k(1);
+      store_k(1);
       store_v(0);
-      if (2 < nkb) load_k(2);
-      if (1 < nkb) load_v(1);
+      load_k(min(2, last));
+      load_v(min(1, last));
       floatx16 sacc[2];
       qk(0, sacc);
-      rescale(softmax(0, sacc));
+      if (0 >= kb_diag) mask(0, sacc);
+      rescale(softmax(sacc));
       __syncthreads();
     }
     // Block kb: stage K_{kb+1} and V_kb, fetch K_{kb+2} and V_{kb+1},
@@ -282,20 +298,22 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     // previous barrier, so one barrier per block suffices.
     for (int kb = 1; kb < nkb; ++kb) {
       const int buf = kb & 1;
-      if (kb + 1 < nkb) store_k(buf ^ 1);
+      store_k(buf ^ 1);
       store_v(buf);
-      if (kb + 2 < nkb) load_k(kb + 2);
-      if (kb + 1 < nkb) load_v(kb + 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the refetch behind the stores: one set of staging registers
+      load_k(min(kb + 2, last));
+      load_v(min(kb + 1, last));
       floatx16 sacc[2];
       qk(buf, sacc);
+      if (kb >= kb_diag) mask(kb, sacc);
       pv(buf ^ 1);
-      rescale(softmax(kb, sacc));
+      rescale(softmax(sacc));
       __syncthreads();
     }
     pv((nkb - 1) & 1);
 
     // ---- epilogue: full row sums, normalise, store ---------------------------
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = halves_sum(l_run);
     if (wave_active && my_q < S) {
       const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
       const int64_t orow = (int64_t)my_q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
