@@ -88,6 +88,14 @@ class HipBackend:
             self._ws[key] = ws  # kept until close(): captured graphs may point at it
         return ws
 
+    def _prefill_workspace(self, seqlen: int, kv_heads: int, dim: int) -> torch.Tensor:
+        nbytes = int(self._lib.bt_prefill_workspace_bytes(seqlen, kv_heads, dim))
+        ws = self._ws.get("prefill")
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=self._dev)
+            self._ws["prefill"] = ws  # grows only; kept until close()
+        return ws
+
     @property
     def tile_tokens(self) -> int:
         """Tokens per decode tile; tile t belongs to split t % num_split."""
@@ -303,10 +311,12 @@ class HipBackend:
         if k.stride() != v.stride():
             raise RuntimeError("k and v need identical strides")
         out = torch.empty((steps, heads, dim), dtype=out_dtype, device=self._dev)
+        ws = self._prefill_workspace(steps, groups, dim)
         rc = self._lib.bt_gqa_prefill(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1),
             k.stride(0), k.stride(1), steps, heads, groups, dim, float(scale),
-            out.data_ptr(), _dtype_code(out_dtype), out.stride(0), out.stride(1),
+            ws.data_ptr(), ws.numel(), out.data_ptr(), _dtype_code(out_dtype),
+            out.stride(0), out.stride(1),
             _stream(self._dev),
         )
         check("bt_gqa_prefill", rc)

@@ -64,7 +64,17 @@ struct PrefillParams {
   void* out;
   int out_bf16;
   int64_t out_stride_tok, out_stride_head;
+  uint16_t* vt;        // workspace: fp16 V^T image, prefill_vt_bytes() bytes
 };
+
+// Keys per block of the prefill key loop, and the size of the transposed fp16
+// V image the prefill builds in its workspace: per kv head and 64-key block,
+// 8 chunks of 8 keys x head_dim rows x 16 bytes.
+constexpr int kPrefillKeyBlock = 64;
+inline size_t prefill_vt_bytes(int seqlen, int kv_heads, int head_dim) {
+  const size_t blocks = (size_t)(seqlen + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
+  return (size_t)kv_heads * blocks * kPrefillKeyBlock * (size_t)head_dim * 2;
+}
 
 // Which kernel variant serves a combination of length sources, or -1 if the
 // combination is not served:

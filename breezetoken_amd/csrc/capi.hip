@@ -253,12 +253,17 @@ int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, c
                                total_splits, out, out_dtype, out_stride_seq, stream);
 }
 
+int64_t bt_prefill_workspace_bytes(int32_t seqlen, int32_t kv_heads, int32_t head_dim) {
+  if (seqlen < 1 || kv_heads < 1 || head_dim < 1) return 0;
+  return (int64_t)bt::prefill_vt_bytes(seqlen, kv_heads, head_dim);
+}
+
 int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
                    int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
                    int32_t seqlen, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
-                   void* out, int32_t out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
-                   void* stream) {
-  if (!q || !k || !v || !out) return BT_EINVAL;
+                   void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
+                   int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+  if (!q || !k || !v || !out || !workspace) return BT_EINVAL;
   if (seqlen < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads) return BT_EINVAL;
   if (out_dtype != BT_DTYPE_F32 && out_dtype != BT_DTYPE_BF16) return BT_EINVAL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return BT_EINVAL;
@@ -268,8 +273,16 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   if (q_stride_tok % 8 || q_stride_head % 8 || kv_stride_tok % 8 || kv_stride_head % 8 ||
       out_stride_tok % 8 || out_stride_head % 8)
     return BT_EINVAL;
+  if (!aligned16(workspace)) return BT_EINVAL;
   if (head_dim != 256 && head_dim != 128) return BT_ENOTSUP;
   if (heads / kv_heads > 8) return BT_ENOTSUP;
+  // 32-bit buffer offsets: the K rows of one kv head (plus the last block's
+  // tail) and its V^T image
+  const int64_t nblk = (seqlen + bt::kPrefillKeyBlock - 1) / bt::kPrefillKeyBlock;
+  if ((nblk + 1) * bt::kPrefillKeyBlock * kv_stride_tok * 2 > (int64_t)UINT32_MAX ||
+      nblk * bt::kPrefillKeyBlock * head_dim * 2 > (int64_t)UINT32_MAX)
+    return BT_ENOTSUP;
+  if (workspace_bytes < bt_prefill_workspace_bytes(seqlen, kv_heads, head_dim)) return BT_ENOSPC;
   bt::PrefillParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k);
@@ -287,6 +300,7 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   p.out_bf16 = out_dtype == BT_DTYPE_BF16;
   p.out_stride_tok = out_stride_tok;
   p.out_stride_head = out_stride_head;
+  p.vt = static_cast<uint16_t*>(workspace);
   return hip_rc(bt::launch_prefill(p, head_dim, (hipStream_t)stream));
 }
 

@@ -7,25 +7,30 @@
 // of _prefill_attn (breezetoken/model/prefill.py:56-68).
 //
 // Decomposition (MI355X-first):
+//  * a small pre-pass writes V once per kv head as a transposed fp16 image
+//    (V^T in 8-key chunks; exact for |v| <= 65504, larger values saturate), so
+//    the key loop needs neither a conversion nor a transposing LDS read;
 //  * one work-group (4 waves) per (block of query positions, kv head); wave w
 //    owns query head w of the GQA group (and, for G < 4, a different block of
 //    positions), so every K/V tile staged in LDS feeds all G heads;
-//  * S^T = K . Q^T on v_mfma_f32_32x32x16_bf16: 64 keys x 32 queries per step,
-//    K rows from an XOR-swizzled LDS tile, Q^T held in registers;
-//  * O^T = V^T . P^T on v_mfma_f32_32x32x16_f16: V is converted to fp16 once
-//    when it is staged in LDS (exact for |v| <= 65504, larger values saturate)
-//    and read back with ds_read_b64_tr_b16; P (<= 2^8, see below) is rounded
-//    to fp16 (11-bit mantissa; bf16's 8 bits would put the first rows of the
-//    prompt above a 2e-3 error), and the lane that owns a score column owns the
-//    P^T operand for it, so P never moves between lanes;
+//  * K and V^T tiles go HBM -> LDS by buffer_load ... lds (no staging
+//    registers, no LDS write instructions); K lands chunk-major (16-byte chunk
+//    c of key row r at c * 1024 + r * 16), which keeps the MFMA operand reads
+//    conflict-free and needs only a per-lane row offset on the HBM side;
+//  * S^T = K . Q^T on v_mfma_f32_32x32x16_bf16 (64 keys x 32 queries per
+//    block, Q^T in registers); O^T = V^T . P^T on v_mfma_f32_32x32x16_f16 with
+//    P (<= 2^8, see below) rounded to fp16 -- bf16's 8-bit mantissa would put
+//    the first rows of the prompt above a 2e-3 error -- and the lane that owns
+//    a score column owns the P^T operand for it, so P never moves between lanes;
 //  * online softmax in the log2 domain with lazy rescaling: the reference
 //    maximum only moves (and O^T is only rescaled) when a score exceeds it by
-//    more than 2^8, so most key blocks skip the 128-register rescale;
-//  * software pipeline over 64-key blocks: iteration i stages K_{i+1} and V_i
-//    into LDS and fetches K_{i+2} / V_{i+1} from HBM while multiplying
-//    S_i = K_i . Q^T, then runs the softmax of S_i next to O += V_{i-1} . P_{i-1},
-//    so matrix-core work always has independent VALU/LDS work beside it; every
-//    buffer is rewritten only after the barrier that ends its last reader;
+//    more than 2^8, so almost every key block skips the 128-register rescale;
+//    only blocks that reach past a wave's first query apply the causal mask;
+//  * double-buffered tiles: the step of key block kb starts the copies of
+//    K_{kb+1} and V_kb, multiplies S_kb = K_kb . Q^T and O += V_{kb-1} . P_{kb-1},
+//    runs the softmax of S_kb, then waits for its copies and meets the
+//    work-group barrier; a buffer is rewritten only after the barrier that
+//    ends its last reader;
 //  * heavy (late) query blocks are launched first to balance the causal work.
 #include "bt_common.h"
 #include "bt_kernels.h"
@@ -35,12 +40,14 @@ namespace bt {
 namespace {
 
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float float2v __attribute__((ext_vector_type(2)));
 
+template <int B>
+struct Buf {
+  static constexpr int value = B;
+};
 
-constexpr int kQB = 32;      // query positions per wave
-constexpr int kKB = 64;      // keys per step
+constexpr int kQB = 32;                 // query positions per wave
+constexpr int kKB = kPrefillKeyBlock;   // keys per block (64)
 constexpr int kWaves = 4;
 constexpr float kLazy = 8.0f;  // log2-domain slack before the reference max moves
 
@@ -55,28 +62,86 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
 }
+// HBM -> LDS copy of 16 bytes per lane: lane l's bytes at voff + soff land at
+// lds + 16 * l (lds is wave-uniform).  Offsets past the descriptor's range
+// (soffset included) read as zero.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (BT_LDS void*)lds, 16, (int)voff, (int)soff, 0, 0);
+}
 
 // Two floats -> packed fp16 pair, round toward zero (bf16 values convert exactly;
 // out-of-range magnitudes saturate to +-65504 instead of becoming inf).
 __device__ __forceinline__ uint32_t pack_f16_rtz(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
-// Two floats -> packed fp16 pair, round to nearest even (one v_cvt_pk_f16_f32).
+// Two floats -> packed fp16 pair, round to nearest even, with one
+// v_cvt_pk_f16_f32.  Written as asm because the equivalent vector convert
+// lets the scheduler hoist the whole softmax and overflow the register file.
 __device__ __forceinline__ uint32_t pack_f16_rne(float a, float b) {
   uint32_t r;
   asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
 
-__device__ __forceinline__ u32x4 bf16x8_to_f16x8(const u32x4& v) {
-  u32x4 r;
+// Instruction-group ordering for the scheduler (masks: 0x2 VALU, 0x8 MFMA,
+// 0x100 DS read).  With one wave per SIMD the matrix core only overlaps VALU
+// and LDS work that sits between MFMAs in program order, so each MFMA is
+// followed by a share of the independent work.
+template <int kMfma, int kAhead, int kValu, int kVmem>
+__device__ __forceinline__ void interleave() {
+  __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);  // operands of the first MFMAs
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    r[i] = pack_f16_rtz(__uint_as_float(v[i] << 16), __uint_as_float(v[i] & 0xffff0000u));
-  return r;
+  for (int i = 0; i < kMfma; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i + kAhead < kMfma) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if (kValu) __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
+    if (kVmem && i < kVmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+  }
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Pre-pass: V (S, Hkv, D) bf16 -> fp16 V^T image.  Key block b of kv head g is
+// stored at vt + (g * nblk + b) * 64 * D as 8 key chunks; chunk c = 2 * ks + h
+// holds, for every d, the values V[b*64 + key][d] of the 8 keys
+//     key = ks*16 + h*4 + {0, 1, 2, 3, 8, 9, 10, 11}
+// (16 bytes) at row d.  That is the key order in which lane l of the P^T
+// operand holds P: the 32x32 MFMA result puts key (j/4)*8 + (l/32)*4 + j%4 of
+// a 32-key half in register j, and each 16-key step takes 8 consecutive
+// registers.  Keys past the prompt are zero.  Each thread transposes 8 x 8
+// tiles (one chunk, dims dc*8..) in registers.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_vt_kernel(PrefillParams p) {
+  constexpr int kDC = D / 8;
+  const int blk = blockIdx.x, g = blockIdx.y;
+  const int nblk = gridDim.x;
+  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+  const __amdgpu_buffer_rsrc_t vrs =
+      make_rsrc(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)p.seqlen * row_bytes);
+  uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kKB * D;
+  for (int item = threadIdx.x; item < 8 * kDC; item += 256) {
+    const int c = item / kDC, dc = item % kDC;
+    u32x4 rows[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = blk * kKB + (c >> 1) * 16 + (c & 1) * 4 + (j & 3) + (j >> 2) * 8;
+      rows[j] = buf_load16(vrs, (uint32_t)key * row_bytes + (uint32_t)dc * 16, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // output row d = dc*8 + i
+      u32x4 o;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t w0 = rows[2 * m][i >> 1], w1 = rows[2 * m + 1][i >> 1];
+        const float f0 = __uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16));
+        const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
+        o[m] = pack_f16_rtz(f0, f1);
+      }
+      *reinterpret_cast<u32x4*>(img + ((size_t)c * D + dc * 8 + i) * 8) = o;
+    }
+  }
+}
 
 // D: head dim (128 or 256).  Wave w of a work-group handles query head
 // (pass * 4 + w % GW) of the group and positions [q0 + (w / GW) * 32, +32),
@@ -85,23 +150,25 @@ template <int D>
 __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillParams p) {
   constexpr int kSteps = D / 16;       // K-dimension steps of Q.K^T (16 per MFMA)
   constexpr int kDTiles = D / 32;      // 32-wide d tiles of O^T
-  constexpr int kRowBytes = D * 2;
-  constexpr int kChunks = D / 8;       // 16-byte chunks per row
-  constexpr int kTileBytes = kKB * kRowBytes;
-  constexpr int kLoads = kTileBytes / (16 * kWaves * 64);  // 16-byte loads per thread per tile
-  // Padded LDS rows instead of XOR swizzles, so every per-step offset is an
-  // immediate: K rows step 16 B past a multiple of 256 B (16 consecutive rows hit
-  // 16 different bank groups for 16-byte reads); V rows step 64 B (the 4 rows of
-  // a transposed read land in 4 different 64-byte bank windows).
-  constexpr int kKStride = kRowBytes + 16;
-  constexpr int kVStride = kRowBytes + 64;
-  constexpr int kKTile = kKB * kKStride;
-  constexpr int kVTile = kKB * kVStride;
-  constexpr int kBufBytes = kKTile + kVTile;
+  constexpr int kImg = kKB * D * 2;    // bytes of one K or V^T tile
+  constexpr int kCopies = kImg / 1024 / kWaves;  // 1 KiB copies per wave per tile
 
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kBufBytes];  // K0 V0 K1 V1
+  // Four separate LDS arrays (not offsets into one) so the compiler can see
+  // that copies into one buffer never alias MFMA operand reads from another:
+  // it neither orders them nor waits for the copies before those reads.  The
+  // key loop is unrolled by two so every buffer choice is a constant.
+  __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[kImg];
+  __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[kImg];
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kImg];
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[kImg];
+  auto k_buf = [&](auto b) -> unsigned char* {
+    if constexpr (decltype(b)::value == 0) return k_lds0; else return k_lds1;
+  };
+  auto v_buf = [&](auto b) -> unsigned char* {
+    if constexpr (decltype(b)::value == 0) return v_lds0; else return v_lds1;
+  };
 
-  asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.v), "s"(p.out), "s"(p.seqlen), "s"(p.group),
+  asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.vt), "s"(p.out), "s"(p.seqlen), "s"(p.group),
                "s"(p.q_stride_tok), "s"(p.q_stride_head), "s"(p.kv_stride_tok), "s"(p.kv_stride_head),
                "s"(p.out_stride_tok), "s"(p.out_stride_head), "s"(p.scale_log2));
   const int t = threadIdx.x;
@@ -111,53 +178,47 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
   const int G = p.group;
   const int GW = G < kWaves ? G : kWaves;
   const int pos_per_wg = kQB * (kWaves / GW);
-  const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
-  const int qblk = nqb - 1 - (int)blockIdx.x;  // heavy blocks first
   const int S = p.seqlen;
+  const int nqb = (S + pos_per_wg - 1) / pos_per_wg;
+  const int nblk = (S + kKB - 1) / kKB;
+  const int qblk = nqb - 1 - (int)blockIdx.x;  // heavy blocks first
   const int wg_q0 = qblk * pos_per_wg;
   const int q0 = wg_q0 + (wave / GW) * kQB;   // this wave's first position
   const int wg_qend = min(S, wg_q0 + pos_per_wg);
   // keys needed by the work-group: [0, wg_qend)
   const int nkb = (wg_qend + kKB - 1) / kKB;
+  const int last = nkb - 1;
 
+  // Tile copies.  K copy i (1 KiB) is 16-byte chunk i of the 64 key rows, lane
+  // l taking row l; V^T copy i is bytes [1024 i, +1024) of the block's image.
+  // Wave w issues copies w, w + 4, ...
   const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)S * row_bytes);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.v + (int64_t)kvh * p.kv_stride_head, (uint32_t)S * row_bytes);
-
-  // Staging: at step i thread t moves chunk (t % kChunks) of row i * kRowsPerStep + t / kChunks;
-  // the lane part of every address is computed once, the step part is an
-  // immediate (LDS) or a scalar offset (global).
-  constexpr int kRowsPerStep = kWaves * 64 / kChunks;
-  const uint32_t g_lane = (uint32_t)(t / kChunks) * row_bytes + (t % kChunks) * 16;
-  const int k_lane = (t / kChunks) * kKStride + (t % kChunks) * 16;
-  const int v_lane = (t / kChunks) * kVStride + (t % kChunks) * 16;
-  u32x4 kst[kLoads], vst[kLoads];
-  auto load_k = [&](int kb) {
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.vt + (size_t)kvh * nblk * kKB * D, (uint32_t)nblk * kImg);
+  const uint32_t k_voff = (uint32_t)lane * row_bytes;
+  const uint32_t v_voff = (uint32_t)lane * 16;
+  auto copy_k = [&](auto b, int kb) {
     const uint32_t so = (uint32_t)(kb * kKB) * row_bytes;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) kst[i] = buf_load16(krs, g_lane, so + (uint32_t)(i * kRowsPerStep) * row_bytes);
+    for (int j = 0; j < kCopies; ++j) {
+      const int i = wave + kWaves * j;
+      dma16(krs, k_buf(b) + i * 1024, k_voff, so + (uint32_t)i * 16);
+    }
   };
-  auto load_v = [&](int kb) {
-    const uint32_t so = (uint32_t)(kb * kKB) * row_bytes;
+  auto copy_v = [&](auto b, int kb) {
+    const uint32_t so = (uint32_t)kb * kImg;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) vst[i] = buf_load16(vrs, g_lane, so + (uint32_t)(i * kRowsPerStep) * row_bytes);
+    for (int j = 0; j < kCopies; ++j) {
+      const int i = wave + kWaves * j;
+      dma16(vrs, v_buf(b) + i * 1024, v_voff, so + (uint32_t)i * 1024);
+    }
   };
-  auto store_k = [&](int buf) {
-    unsigned char* dst = smem + buf * kBufBytes + k_lane;
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) *reinterpret_cast<u32x4*>(dst + i * kRowsPerStep * kKStride) = kst[i];
-  };
-  auto store_v = [&](int buf) {
-    unsigned char* dst = smem + buf * kBufBytes + kKTile + v_lane;
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i)
-      *reinterpret_cast<u32x4*>(dst + i * kRowsPerStep * kVStride) = bf16x8_to_f16x8(vst[i]);
-  };
+  // Each wave waits for its own copies (vmcnt(0)); the barrier that follows
+  // publishes them to the other waves.
+  auto wait_copies = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };
 
   const int qcol = lane & 31;       // this lane's query column
   const int kgrp = lane >> 5;       // k-slot group of MFMA operands
-  const int i16 = lane & 15;
-  const int sub16 = (lane >> 4) & 1;
   const float c_log2 = p.scale_log2;
 
   const int passes = (G + kWaves - 1) / kWaves;
@@ -188,9 +249,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     const int my_q = q0 + qcol;
     uint32_t pk[2][8];        // P of the latest key block (fp16 pairs)
 
-    // S^T (64 keys x 32 queries) = K . Q^T from K buffer `buf`.
-    auto qk = [&](int buf, floatx16 (&sacc)[2]) {
-      const unsigned char* krow = smem + buf * kBufBytes + qcol * kKStride + kgrp * 16;
+    // S^T (64 keys x 32 queries) = K . Q^T from K buffer b: the A operand of
+    // step st / key half mt is chunk 2*st + kgrp of key row mt*32 + qcol.
+    auto qk = [&](auto b, floatx16 (&sacc)[2]) {
+      const unsigned char* krow = k_buf(b) + kgrp * 1024 + qcol * 16;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -199,25 +261,24 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       for (int st = 0; st < kSteps; ++st) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(krow + mt * 32 * kKStride + st * 32);
+          const u32x4 a = *reinterpret_cast<const u32x4*>(krow + st * 2048 + mt * 512);
           sacc[mt] = mfma32(as_bf16x8(a), as_bf16x8(qop[st]), sacc[mt]);
         }
       }
     };
-    // O^T += V^T . P^T over the 64 keys held in V buffer `buf`.
-    auto pv = [&](int buf) {
-      const unsigned char* vlane = smem + buf * kBufBytes + kKTile + (kgrp * 4 + (i16 >> 2)) * kVStride +
-                                   (sub16 * 16 + (i16 & 3) * 4) * 2;
+    // O^T += V^T . P^T over the 64 keys of V^T buffer b: the A operand of key
+    // step ks / d tile dt is key chunk 2*ks + kgrp of row dt*32 + (lane % 32),
+    // whose key order matches the P^T operand built from the S^T registers.
+    auto pv = [&](auto b) {
+      const unsigned char* vrow = v_buf(b) + kgrp * (D * 16) + qcol * 16;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int mt = ks >> 1, half = ks & 1;
         const u32x4 pop = {pk[mt][half * 4 + 0], pk[mt][half * 4 + 1], pk[mt][half * 4 + 2], pk[mt][half * 4 + 3]};
 #pragma unroll
         for (int dt = 0; dt < kDTiles; ++dt) {
-          const unsigned char* pa = vlane + ks * 16 * kVStride + dt * 64;
-          const bf16x8 vt = lds_read_tr_pair((const BT_LDS uint16_t*)(const BT_LDS unsigned char*)pa,
-                                             (const BT_LDS uint16_t*)(const BT_LDS unsigned char*)(pa + 8 * kVStride));
-          oacc[dt] = mfma32_f16(__builtin_bit_cast(u32x4, vt), pop, oacc[dt]);
+          const u32x4 a = *reinterpret_cast<const u32x4*>(vrow + ks * 2 * (D * 16) + dt * 512);
+          oacc[dt] = mfma32_f16(a, pop, oacc[dt]);
         }
       }
     };
@@ -269,48 +330,50 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     };
     // Blocks whose last key is <= q0 need no causal mask.
     const int kb_diag = (q0 + 1) / kKB;
-    const int last = nkb - 1;
 
-    // Prologue: K_0 in LDS, K_1 and V_0 in flight.  Fetches past the last
-    // block re-read the last block (min(., last)) and are never consumed, so
-    // the key loop has no branches around its loads and stores.
-    load_k(0);
-    load_v(0);
-    store_k(0);
-    load_k(min(1, last));
+    // Prologue: K_0 and V_0 in LDS.
+    copy_k(Buf<0>{}, 0);
+    copy_v(Buf<0>{}, 0);
+    wait_copies();
     __syncthreads();
 
-    // Block 0: stage K_1 / V_0, S_0, softmax -> P_0.
+    // Block 0: copy K_1, S_0, softmax -> P_0.  Copies past the last block
+    // re-read the last block (min(., last)) into a buffer nobody reads, so the
+    // key loop has no branches around its copies.
     {
-      store_k(1);
-      store_v(0);
-      load_k(min(2, last));
-      load_v(min(1, last));
+      copy_k(Buf<1>{}, min(1, last));
       floatx16 sacc[2];
-      qk(0, sacc);
+      qk(Buf<0>{}, sacc);
       if (0 >= kb_diag) mask(0, sacc);
       rescale(softmax(sacc));
+      wait_copies();
       __syncthreads();
     }
-    // Block kb: stage K_{kb+1} and V_kb, fetch K_{kb+2} and V_{kb+1},
-    // S_kb = K_kb . Q^T, O += V_{kb-1} . P_{kb-1}, softmax(S_kb) -> P_kb.
-    // Buffers written here (K (kb+1)%2, V kb%2) were last read before the
-    // previous barrier, so one barrier per block suffices.
-    for (int kb = 1; kb < nkb; ++kb) {
-      const int buf = kb & 1;
-      store_k(buf ^ 1);
-      store_v(buf);
-      __builtin_amdgcn_sched_barrier(0);  // keep the refetch behind the stores: one set of staging registers
-      load_k(min(kb + 2, last));
-      load_v(min(kb + 1, last));
+    // Block kb (buffer b = kb % 2): copy K_{kb+1} -> K buffer b^1 and
+    // V_kb -> V buffer b, S_kb = K_kb . Q^T, O += V_{kb-1} . P_{kb-1},
+    // softmax(S_kb) -> P_kb.  K buffer b^1 was last read by S_{kb-1} and V
+    // buffer b by O += V_{kb-2} . P_{kb-2}, both before the previous barrier.
+    auto step = [&](auto b, int kb) {
+      constexpr int B = decltype(b)::value;
+      copy_k(Buf<B ^ 1>{}, min(kb + 1, last));
+      copy_v(b, kb);
       floatx16 sacc[2];
-      qk(buf, sacc);
+      qk(b, sacc);
+      interleave<kSteps * 2, 4, 0, 2 * kCopies>();
       if (kb >= kb_diag) mask(kb, sacc);
-      pv(buf ^ 1);
-      rescale(softmax(sacc));
+      pv(Buf<B ^ 1>{});
+      const float alpha = softmax(sacc);
+      interleave<kDTiles * 4, 4, 4, 0>();
+      rescale(alpha);
+      wait_copies();
       __syncthreads();
+    };
+    for (int kb = 1; kb < nkb; kb += 2) {
+      step(Buf<1>{}, kb);
+      if (kb + 1 < nkb) step(Buf<0>{}, kb + 1);
     }
-    pv((nkb - 1) & 1);
+    // V_last arrived in buffer last % 2 (the prologue's V_0 when nkb == 1).
+    if (last & 1) pv(Buf<1>{}); else pv(Buf<0>{});
 
     // ---- epilogue: full row sums, normalise, store ---------------------------
     l_run = halves_sum(l_run);
@@ -334,7 +397,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
         }
       }
     }
-    __syncthreads();  // the next pass restages buffer 0
+    __syncthreads();  // the next pass recopies buffers 0 and 1
   }
 }
 
@@ -343,10 +406,17 @@ hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stre
   const int GW = G < kWaves ? G : kWaves;
   const int pos_per_wg = kQB * (kWaves / GW);
   const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
-  dim3 grid(nqb, p.kv_heads);
+  const int nblk = (p.seqlen + kKB - 1) / kKB;
+  const dim3 grid(nqb, p.kv_heads), vt_grid(nblk, p.kv_heads);
   switch (head_dim) {
-    case 128: hipLaunchKernelGGL(gqa_prefill_kernel<128>, grid, dim3(kWaves * 64), 0, stream, p); break;
-    case 256: hipLaunchKernelGGL(gqa_prefill_kernel<256>, grid, dim3(kWaves * 64), 0, stream, p); break;
+    case 128:
+      hipLaunchKernelGGL(prefill_vt_kernel<128>, vt_grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(gqa_prefill_kernel<128>, grid, dim3(kWaves * 64), 0, stream, p);
+      break;
+    case 256:
+      hipLaunchKernelGGL(prefill_vt_kernel<256>, vt_grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(gqa_prefill_kernel<256>, grid, dim3(kWaves * 64), 0, stream, p);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -121,17 +121,26 @@ int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, c
                          void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
                          int64_t out_stride_seq, void* stream);
 
+/* Bytes of prefill workspace (the transposed fp16 V image the prefill builds
+ * once per call) for a prompt of `seqlen` tokens; 0 for invalid arguments.
+ * Like bt_decode_workspace_bytes it replaces a per-call allocation: the
+ * reference's SDPA call (prefill.py:60-68) allocates its scratch internally. */
+int64_t bt_prefill_workspace_bytes(int32_t seqlen, int32_t kv_heads, int32_t head_dim);
+
 /* Causal GQA prefill attention on bf16 MFMA: replaces the
  * F.scaled_dot_product_attention(is_causal=True, enable_gqa=True) call of
  * _prefill_attn (breezetoken/model/prefill.py:56-68).  q (S, heads, D),
  * k/v (S, kv_heads, D) bf16 with the given strides; query i attends keys 0..i
  * (the prompt starts at slot 0, prefill.py:54-55).  out (S, heads, D) f32 or
- * bf16. */
+ * bf16.  `workspace` (16-byte aligned) must hold
+ * bt_prefill_workspace_bytes(seqlen, kv_heads, head_dim) bytes; it is scratch
+ * for the duration of the call on `stream`. */
 int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
                    int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
                    int32_t seqlen, int32_t heads, int32_t kv_heads, int32_t head_dim,
-                   float scale, void* out, int32_t out_dtype, int64_t out_stride_tok,
-                   int64_t out_stride_head, void* stream);
+                   float scale, void* workspace, int64_t workspace_bytes, void* out,
+                   int32_t out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
+                   void* stream);
 
 #ifdef __cplusplus
 }

@@ -56,6 +56,10 @@ def test_workspace_bytes():
     assert lib.bt_decode_workspace_bytes(8, 256, 128) == 4096 + 8 * 128 * 256 * 4
     assert lib.bt_decode_workspace_bytes(8, 256, 1) == 256 + 8 * 256 * 4
     assert lib.bt_decode_workspace_bytes(0, 256, 1) == 0
+    # prefill: one fp16 V^T image per kv head, whole 64-key blocks
+    assert lib.bt_prefill_workspace_bytes(8192, 2, 256) == 2 * 8192 * 256 * 2
+    assert lib.bt_prefill_workspace_bytes(65, 1, 128) == 128 * 128 * 2
+    assert lib.bt_prefill_workspace_bytes(0, 1, 128) == 0
 
 
 @pytest.mark.parametrize(
@@ -134,10 +138,18 @@ def test_entry_points_refuse_bad_arguments_before_launching():
     rc = lib.bt_gqa_decode_split(fake, 0, 0, fake, fake, 512, 256, None, None, None, 16, 1, 8, 2,
                                  256, 5000, 0.0625, fake, fake, None)
     assert rc == _lib.BT_ENOTSUP
-    # prefill: unserved head dim, bad strides
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 8, 2, 64, 0.125, fake, 0,
-                            2048, 256, None)
+    # prefill: unserved head dim, bad strides, missing or short workspace
+    big = 1 << 30
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 8, 2, 64, 0.125, fake, big,
+                            fake, 0, 2048, 256, None)
     assert rc == _lib.BT_ENOTSUP
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 0, 8, 2, 256, 0.0625, fake, 0,
-                            2048, 256, None)
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 0, 8, 2, 256, 0.0625, fake, big,
+                            fake, 0, 2048, 256, None)
     assert rc == _lib.BT_EINVAL
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 8, 2, 256, 0.0625, None, big,
+                            fake, 0, 2048, 256, None)
+    assert rc == _lib.BT_EINVAL
+    need = lib.bt_prefill_workspace_bytes(16, 2, 256)
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 8, 2, 256, 0.0625, fake,
+                            need - 1, fake, 0, 2048, 256, None)
+    assert rc == _lib.BT_ENOSPC
