@@ -27,8 +27,10 @@
 //    more than 2^8, so almost every key block skips the 128-register rescale;
 //    only blocks that reach past a wave's first query apply the causal mask;
 //  * double-buffered tiles: the step of key block kb starts the copies of
-//    K_{kb+1} and V_kb, multiplies S_kb = K_kb . Q^T and O += V_{kb-1} . P_{kb-1},
-//    runs the softmax of S_kb, then waits for its copies and meets the
+//    K_{kb+1} and V_kb, multiplies S_kb = K_kb . Q^T beside the exponentials
+//    of the second half of P_{kb-1}, then O += V_{kb-1} . P_{kb-1} beside the
+//    max and first-half exponentials of S_kb, so both matrix-core phases have
+//    VALU work interleaved; it then waits for its copies and meets the
 //    work-group barrier; a buffer is rewritten only after the barrier that
 //    ends its last reader;
 //  * heavy (late) query blocks are launched first to balance the causal work.
@@ -40,6 +42,8 @@ namespace bt {
 namespace {
 
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 
 template <int B>
 struct Buf {
@@ -74,13 +78,11 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* l
 __device__ __forceinline__ uint32_t pack_f16_rtz(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
-// Two floats -> packed fp16 pair, round to nearest even, with one
-// v_cvt_pk_f16_f32.  Written as asm because the equivalent vector convert
-// lets the scheduler hoist the whole softmax and overflow the register file.
+// Two floats -> packed fp16 pair, round to nearest even (one v_cvt_pk_f16_f32).
+// A builtin, not asm: the compiler must see this VALU write to insert the wait
+// states a VGPR needs after an in-flight MFMA has read it as an operand.
 __device__ __forceinline__ uint32_t pack_f16_rne(float a, float b) {
-  uint32_t r;
-  asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2v){a, b}, half2v));
 }
 
 // Instruction-group ordering for the scheduler (masks: 0x2 VALU, 0x8 MFMA,
@@ -247,7 +249,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     float m_ref = -INFINITY;  // reference max (log2 domain) of this lane's column
     float l_run = 0.f;        // partial row sum over this lane's keys
     const int my_q = q0 + qcol;
-    uint32_t pk[2][8];        // P of the latest key block (fp16 pairs)
+    // P of a key block as fp16 pairs: pk0 holds keys 0..31 of the block, pk1
+    // keys 32..63 (the two 32-key halves of the S^T registers).
+    uint32_t pk0[8], pk1[8];
+    floatx16 s_tail;          // S^T of the latest block's keys 32..63, pending exp
+    float neg_m_tail = 0.f;   // -reference max those scores are exponentiated with
 
     // S^T (64 keys x 32 queries) = K . Q^T from K buffer b: the A operand of
     // step st / key half mt is chunk 2*st + kgrp of key row mt*32 + qcol.
@@ -269,12 +275,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     // O^T += V^T . P^T over the 64 keys of V^T buffer b: the A operand of key
     // step ks / d tile dt is key chunk 2*ks + kgrp of row dt*32 + (lane % 32),
     // whose key order matches the P^T operand built from the S^T registers.
-    auto pv = [&](auto b) {
+    auto pv = [&](auto b, const uint32_t(&p0)[8], const uint32_t(&p1)[8]) {
       const unsigned char* vrow = v_buf(b) + kgrp * (D * 16) + qcol * 16;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const int mt = ks >> 1, half = ks & 1;
-        const u32x4 pop = {pk[mt][half * 4 + 0], pk[mt][half * 4 + 1], pk[mt][half * 4 + 2], pk[mt][half * 4 + 3]};
+        const uint32_t* ph = (ks < 2 ? p0 : p1) + (ks & 1) * 4;
+        const u32x4 pop = {ph[0], ph[1], ph[2], ph[3]};
 #pragma unroll
         for (int dt = 0; dt < kDTiles; ++dt) {
           const u32x4 a = *reinterpret_cast<const u32x4*>(vrow + ks * 2 * (D * 16) + dt * 512);
@@ -293,10 +299,23 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
           sacc[mt][j] = key <= my_q ? sacc[mt][j] : -INFINITY;
         }
     };
-    // Online softmax of one block: fills pk and returns the factor the
-    // accumulated O must be scaled by (1 unless the reference max moved).
-    // Scores stay unscaled until exp2(s * c - m).
-    auto softmax = [&](floatx16(&sacc)[2]) -> float {
+    // exp2(s * c - m) of one 32-key half into fp16 pairs; returns the sum.
+    auto exp_half = [&](const floatx16& s, float neg_m, uint32_t(&out)[8]) -> float {
+      float psum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; j += 2) {
+        const float p0 = fast_exp2(fmaf(s[j], c_log2, neg_m));
+        const float p1 = fast_exp2(fmaf(s[j + 1], c_log2, neg_m));
+        psum += p0 + p1;
+        out[j / 2] = pack_f16_rne(p0, p1);
+      }
+      return psum;
+    };
+    // Online softmax, first part: block max, lazy reference-max update, P of
+    // keys 0..31 into out.  Returns the factor the accumulated O must be
+    // scaled by (1 unless the reference max moved).  Keys 32..63 follow in
+    // softmax_tail beside the next block's S = K.Q^T.
+    auto softmax_head = [&](floatx16(&sacc)[2], uint32_t(&out)[8]) -> float {
       float tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -308,20 +327,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       const float m_new = move ? tmax : m_ref;
       const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
       m_ref = m_new;
-      const float neg_m = m_ref == -INFINITY ? 0.f : -m_ref;
-      float psum = 0.f;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          const float p0 = fast_exp2(fmaf(sacc[mt][j], c_log2, neg_m));
-          const float p1 = fast_exp2(fmaf(sacc[mt][j + 1], c_log2, neg_m));
-          psum += p0 + p1;
-          pk[mt][j / 2] = pack_f16_rne(p0, p1);
-        }
-      l_run = l_run * alpha + psum;
+      neg_m_tail = m_ref == -INFINITY ? 0.f : -m_ref;
+      l_run = l_run * alpha + exp_half(sacc[0], neg_m_tail, out);
+      s_tail = sacc[1];
       return alpha;
     };
+    auto softmax_tail = [&] { l_run += exp_half(s_tail, neg_m_tail, pk1); };
     auto rescale = [&](float alpha) {
       if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max moved by > 2^8
 #pragma unroll
@@ -337,7 +348,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     wait_copies();
     __syncthreads();
 
-    // Block 0: copy K_1, S_0, softmax -> P_0.  Copies past the last block
+    // Block 0: copy K_1, S_0, first softmax part.  Copies past the last block
     // re-read the last block (min(., last)) into a buffer nobody reads, so the
     // key loop has no branches around its copies.
     {
@@ -345,26 +356,33 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       floatx16 sacc[2];
       qk(Buf<0>{}, sacc);
       if (0 >= kb_diag) mask(0, sacc);
-      rescale(softmax(sacc));
+      rescale(softmax_head(sacc, pk0));
       wait_copies();
       __syncthreads();
     }
-    // Block kb (buffer b = kb % 2): copy K_{kb+1} -> K buffer b^1 and
-    // V_kb -> V buffer b, S_kb = K_kb . Q^T, O += V_{kb-1} . P_{kb-1},
-    // softmax(S_kb) -> P_kb.  K buffer b^1 was last read by S_{kb-1} and V
-    // buffer b by O += V_{kb-2} . P_{kb-2}, both before the previous barrier.
+    // Block kb (buffer b = kb % 2), two matrix-core phases with VALU work
+    // beside each:
+    //   A: S_kb = K_kb . Q^T       beside  P_{kb-1} of keys 32..63
+    //   B: O += V_{kb-1} . P_{kb-1} beside  max of S_kb, P_kb of keys 0..31
+    // plus the copies K_{kb+1} -> K buffer b^1 and V_kb -> V buffer b.  K
+    // buffer b^1 was last read by S_{kb-1} and V buffer b by O += V_{kb-2} .
+    // P_{kb-2}, both before the previous barrier.
     auto step = [&](auto b, int kb) {
       constexpr int B = decltype(b)::value;
       copy_k(Buf<B ^ 1>{}, min(kb + 1, last));
       copy_v(b, kb);
       floatx16 sacc[2];
       qk(b, sacc);
-      interleave<kSteps * 2, 4, 0, 2 * kCopies>();
+      softmax_tail();
+      interleave<kSteps * 2, 4, 2, 2 * kCopies>();
       if (kb >= kb_diag) mask(kb, sacc);
-      pv(Buf<B ^ 1>{});
-      const float alpha = softmax(sacc);
+      pv(Buf<B ^ 1>{}, pk0, pk1);
+      uint32_t pk0_next[8];
+      const float alpha = softmax_head(sacc, pk0_next);
       interleave<kDTiles * 4, 4, 4, 0>();
       rescale(alpha);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pk0[i] = pk0_next[i];
       wait_copies();
       __syncthreads();
     };
@@ -372,8 +390,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       step(Buf<1>{}, kb);
       if (kb + 1 < nkb) step(Buf<0>{}, kb + 1);
     }
-    // V_last arrived in buffer last % 2 (the prologue's V_0 when nkb == 1).
-    if (last & 1) pv(Buf<1>{}); else pv(Buf<0>{});
+    // P of the last block, keys 32..63; V_last arrived in buffer last % 2
+    // (the prologue's V_0 when nkb == 1).
+    softmax_tail();
+    if (last & 1) pv(Buf<1>{}, pk0, pk1); else pv(Buf<0>{}, pk0, pk1);
 
     // ---- epilogue: full row sums, normalise, store ---------------------------
     l_run = halves_sum(l_run);
