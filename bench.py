@@ -84,7 +84,7 @@ def pmc_mode(torch, backend, dev) -> int:
     src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device=dev).normal_()
     dst = torch.empty_like(src)
     for _ in range(5):
-        dst.copy_(src)  # 256 MiB read + 256 MiB written per launch
+        torch.mul(src, 2.0, out=dst)  # MulFunctor kernel: 256 MiB read + 256 MiB written
     case = wl.c2_inputs(L, cap=CAP)
     ns = backend.pick_splits(HKV, CAP)
     lse = torch.empty((H, ns), dtype=torch.float32, device=dev)
@@ -106,8 +106,31 @@ def pmc_mode(torch, backend, dev) -> int:
                 lse.data_ptr(), part.data_ptr(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
             _lib.check("bt_gqa_decode_split", rc)
     torch.cuda.synchronize()
-    print(json.dumps({"mode": "pmc", "copy_bytes_each_way": src.numel() * 2,
+    print(json.dumps({"mode": "pmc", "copy_kernel": "MulFunctor", "copy_bytes_each_way": src.numel() * 2,
                       "split_algorithmic_bytes": 2 * L * HKV * D * 2 + H * D * 4}), flush=True)
+    return 0
+
+
+def prefill_mode(torch, backend, dev, calls: int) -> int:
+    """Config-4 prefill at S=8192 only (for rocprofv3 kernel traces): ``calls``
+    calls after two warm-up calls, timed with HIP events on the current stream."""
+    from breezetoken_amd import workloads as wl
+
+    q, k, v, scale = wl.c4_inputs(8192)
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    for _ in range(2):
+        backend.attention_prefill(q, k, v, scale, torch.bfloat16)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(torch.cuda.current_stream())
+    for _ in range(calls):
+        backend.attention_prefill(q, k, v, scale, torch.bfloat16)
+    end.record(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / calls
+    fl = wl.prefill_flops(8192, 8, 256)
+    print(json.dumps({"mode": "prefill", "steps": 8192, "calls": calls, "us_per_call": round(us, 2),
+                      "TFLOPs": round(fl / us / 1e6, 1)}), flush=True)
     return 0
 
 
@@ -119,9 +142,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--mode", choices=["bench", "pmc"], default="bench",
+    ap.add_argument("--mode", choices=["bench", "pmc", "prefill"], default="bench",
                     help="pmc: only a 256 MiB device copy and the config-2 split kernel, "
-                         "5 launches each, for rocprofv3 --pmc runs")
+                         "5 launches each, for rocprofv3 --pmc runs; prefill: only config-4 "
+                         "prefill at S=8192 (--steps calls), for kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
         print("this build measures one GPU only: the decode/prefill kernels run on a single "
@@ -145,6 +169,8 @@ def main() -> int:
     H, HKV, D, CAP = 8, 2, 256, 65536
     if args.mode == "pmc":
         return pmc_mode(torch, backend, dev)
+    if args.mode == "prefill":
+        return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)))
 
     def fixed_case(case, cap):
         cache = KVCache(cap, case.k.shape[1], case.k.shape[2], dev)
@@ -281,6 +307,14 @@ def main() -> int:
             pre.append({"steps": s, "us_per_call": pms * 1e3, "TFLOPs": fl / (pms * 1e-3) / 1e12,
                         "frac_bf16_peak": fl / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS})
         extra["c4_prefill"] = pre
+        if pre and "TFLOPs" in pre[-1]:
+            big = pre[-1]
+            # the call = V^T pre-pass + MFMA kernel; both inside the timed region
+            extra["c4_prefill_roofline"] = {
+                "bound": "mfma", "achieved": round(big["TFLOPs"], 1), "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(big["frac_bf16_peak"], 4), "steps": big["steps"],
+                "kernels": "prefill_vt_kernel<256> + gqa_prefill_kernel<256>",
+                "algorithmic_flops": wl.prefill_flops(big["steps"], 8, 256)}
         log("c4: " + json.dumps(pre))
 
     # ------------------------------------------------------------ CPU baseline
