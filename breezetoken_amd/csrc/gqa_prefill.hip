@@ -26,13 +26,14 @@
 //    maximum only moves (and O^T is only rescaled) when a score exceeds it by
 //    more than 2^8, so almost every key block skips the 128-register rescale;
 //    only blocks that reach past a wave's first query apply the causal mask;
-//  * double-buffered tiles: the step of key block kb starts the copies of
-//    K_{kb+1} and V_kb, multiplies S_kb = K_kb . Q^T beside the exponentials
-//    of the second half of P_{kb-1}, then O += V_{kb-1} . P_{kb-1} beside the
-//    max and first-half exponentials of S_kb, so both matrix-core phases have
-//    VALU work interleaved; it then waits for its copies and meets the
-//    work-group barrier; a buffer is rewritten only after the barrier that
-//    ends its last reader;
+//  * double-buffered tiles with two barriers per 64-key step: the step of
+//    block kb multiplies S_kb = K_kb . Q^T beside the exponentials of the
+//    second half of P_{kb-1}, then O += V_{kb-1} . P_{kb-1} beside the max and
+//    first-half exponentials of S_kb, so both matrix-core phases have VALU
+//    work interleaved.  Each tile copy is issued as soon as the barrier that
+//    ends its buffer's last reader has passed (V_kb at the start of step kb,
+//    K_{kb+2} at its middle), so a copy has about one and a half steps to
+//    land before the barrier that publishes it;
 //  * heavy (late) query blocks are launched first to balance the causal work.
 #include "bt_common.h"
 #include "bt_kernels.h"
@@ -215,9 +216,19 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       dma16(vrs, v_buf(b) + i * 1024, v_voff, so + (uint32_t)i * 1024);
     }
   };
-  // Each wave waits for its own copies (vmcnt(0)); the barrier that follows
-  // publishes them to the other waves.
-  auto wait_copies = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };
+  // Each wave waits for its own copies; the barrier that follows publishes
+  // them to the other waves.  wait_all: vmcnt(0).  wait_older: all but the
+  // 2 * kCopies youngest copies of this wave (the two tiles issued since).
+  auto wait_all = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };
+  constexpr int kYoung = 2 * kCopies;
+  constexpr int kWaitOlder = 0x0f70 | (kYoung & 0xf) | ((kYoung >> 4) << 14);
+  static_assert(kYoung < 64, "vmcnt holds 6 bits");
+  auto wait_older = [] { __builtin_amdgcn_s_waitcnt(kWaitOlder); };
+  // Work-group barrier without the release/acquire fence of __syncthreads:
+  // that fence would wait for every copy in flight (vmcnt(0)), while the waits
+  // above need only the tiles the next phase reads.  The LDS reads before it
+  // have all been consumed by MFMAs; lgkmcnt(0) makes that explicit.
+  auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
   const int qcol = lane & 31;       // this lane's query column
   const int kgrp = lane >> 5;       // k-slot group of MFMA operands
@@ -342,54 +353,61 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     // Blocks whose last key is <= q0 need no causal mask.
     const int kb_diag = (q0 + 1) / kKB;
 
-    // Prologue: K_0 and V_0 in LDS.
+    // Copy schedule (double-buffered tiles, copies issued as soon as their
+    // buffer is free, so each has about one and a half steps to land):
+    //   start of step kb:       V_kb      -> V buffer kb % 2 (held V_{kb-2}, read in step kb-1)
+    //   after the mid barrier:  K_{kb+2}  -> K buffer kb % 2 (held K_kb, read in phase A)
+    //   mid barrier of step kb: V_{kb-1} has landed (all but the 2 youngest tiles)
+    //   end barrier of step kb: K_{kb+1} has landed (likewise)
+    // Copies past the last block re-read the last block (min(., last)) into a
+    // buffer nobody reads, so the key loop has no branches around its copies.
     copy_k(Buf<0>{}, 0);
+    copy_k(Buf<1>{}, min(1, last));
     copy_v(Buf<0>{}, 0);
-    wait_copies();
+    wait_all();
     __syncthreads();
 
-    // Block 0: copy K_1, S_0, first softmax part.  Copies past the last block
-    // re-read the last block (min(., last)) into a buffer nobody reads, so the
-    // key loop has no branches around its copies.
+    // Block 0: S_0, then K_2 into K buffer 0, first softmax part.
     {
-      copy_k(Buf<1>{}, min(1, last));
       floatx16 sacc[2];
       qk(Buf<0>{}, sacc);
+      barrier();  // every wave is done reading K_0
+      copy_k(Buf<0>{}, min(2, last));
       if (0 >= kb_diag) mask(0, sacc);
       rescale(softmax_head(sacc, pk0));
-      wait_copies();
-      __syncthreads();
+      barrier();  // K_1 landed in the prologue
     }
     // Block kb (buffer b = kb % 2), two matrix-core phases with VALU work
     // beside each:
     //   A: S_kb = K_kb . Q^T       beside  P_{kb-1} of keys 32..63
     //   B: O += V_{kb-1} . P_{kb-1} beside  max of S_kb, P_kb of keys 0..31
-    // plus the copies K_{kb+1} -> K buffer b^1 and V_kb -> V buffer b.  K
-    // buffer b^1 was last read by S_{kb-1} and V buffer b by O += V_{kb-2} .
-    // P_{kb-2}, both before the previous barrier.
     auto step = [&](auto b, int kb) {
       constexpr int B = decltype(b)::value;
-      copy_k(Buf<B ^ 1>{}, min(kb + 1, last));
       copy_v(b, kb);
       floatx16 sacc[2];
       qk(b, sacc);
       softmax_tail();
-      interleave<kSteps * 2, 4, 2, 2 * kCopies>();
+      interleave<kSteps * 2, 4, 2, kCopies>();
+      wait_older();  // V_{kb-1}
+      barrier();
+      copy_k(b, min(kb + 2, last));
       if (kb >= kb_diag) mask(kb, sacc);
       pv(Buf<B ^ 1>{}, pk0, pk1);
       uint32_t pk0_next[8];
       const float alpha = softmax_head(sacc, pk0_next);
-      interleave<kDTiles * 4, 4, 4, 0>();
+      interleave<kDTiles * 4, 4, 4, kCopies>();
       rescale(alpha);
 #pragma unroll
       for (int i = 0; i < 8; ++i) pk0[i] = pk0_next[i];
-      wait_copies();
-      __syncthreads();
+      wait_older();  // K_{kb+1}
+      barrier();
     };
     for (int kb = 1; kb < nkb; kb += 2) {
       step(Buf<1>{}, kb);
       if (kb + 1 < nkb) step(Buf<0>{}, kb + 1);
     }
+    wait_all();  // V_last (and the last, unread K copy)
+    barrier();
     // P of the last block, keys 32..63; V_last arrived in buffer last % 2
     // (the prologue's V_0 when nkb == 1).
     softmax_tail();
@@ -417,7 +435,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
         }
       }
     }
-    __syncthreads();  // the next pass recopies buffers 0 and 1
+    __syncthreads();  // the next pass recopies all four buffers
   }
 }
 
