@@ -12,9 +12,11 @@ and shapes, so the Qwen3.5 attention layers call it unchanged:
 
 and adds the operators the reference runs outside the protocol:
 
-* ``attention_prefill(q, k, v, scale)``: causal GQA over a prompt that starts
-  at slot 0, q (S, H, D), k/v (S, Hkv, D) -> (S, H, D) (the SDPA call of
-  prefill.py:56-68); ``sdpa_prefill`` takes that call's (1, H, S, D) layout;
+* ``attention_prefill(q, k, v, scale, q_offset=0)``: causal GQA over new
+  tokens at positions q_offset.., q (S, H, D), k/v (q_offset + S, Hkv, D) ->
+  (S, H, D) (the SDPA call of prefill.py:56-68, and with q_offset > 0 the
+  banded chunked prefill of qwen36_moe.py:394-428); ``sdpa_prefill`` takes
+  those calls' (1, H, S, D) layout;
 * ``attention_ragged(...)``: many sequences in one shared cache.
 
 Every launch goes through libbreezetoken_amd.so on torch's current stream with
@@ -292,15 +294,20 @@ class HipBackend:
     # ------------------------------------------------------------------ prefill
     def attention_prefill(
         self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
-        out_dtype: torch.dtype = torch.float32,
+        out_dtype: torch.dtype = torch.float32, q_offset: int = 0,
     ) -> torch.Tensor:
-        """Causal GQA prefill (prefill.py:56-68): q (S, H, D), k/v (S, Hkv, D) bf16 -> (S, H, D)."""
+        """Causal GQA prefill: q (S, H, D) are the new tokens at positions
+        q_offset .. q_offset + S - 1, k/v (q_offset + S, Hkv, D) the cache including
+        them (any token/head strides), all bf16 -> (S, H, D); row i attends keys
+        0 .. q_offset + i.  q_offset = 0 is the SDPA call of prefill.py:56-68, a
+        positive one the banded-mask chunked prefill of qwen36_moe.py:394-428."""
         if q.ndim != 3 or k.ndim != 3 or v.shape != k.shape:
-            raise ValueError("prefill expects q (S, H, D), k/v (S, Hkv, D)")
+            raise ValueError("prefill expects q (S, H, D), k/v (q_offset + S, Hkv, D)")
         steps, heads, dim = q.shape
         groups = k.shape[1]
-        if k.shape[0] != steps or k.shape[2] != dim or heads % groups:
-            raise RuntimeError("prefill q/k/v shapes do not match")
+        q_offset = int(q_offset)
+        if q_offset < 0 or k.shape[0] != q_offset + steps or k.shape[2] != dim or heads % groups:
+            raise RuntimeError("prefill q/k/v shapes do not match (k/v need q_offset + S rows)")
         if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
             raise RuntimeError("the MFMA prefill serves bf16 q/k/v")
         if dim not in SERVED_PREFILL_HEAD_DIMS or heads // groups > MAX_GROUP:
@@ -311,10 +318,10 @@ class HipBackend:
         if k.stride() != v.stride():
             raise RuntimeError("k and v need identical strides")
         out = torch.empty((steps, heads, dim), dtype=out_dtype, device=self._dev)
-        ws = self._prefill_workspace(steps, groups, dim)
+        ws = self._prefill_workspace(q_offset + steps, groups, dim)
         rc = self._lib.bt_gqa_prefill(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1),
-            k.stride(0), k.stride(1), steps, heads, groups, dim, float(scale),
+            k.stride(0), k.stride(1), steps, q_offset, heads, groups, dim, float(scale),
             ws.data_ptr(), ws.numel(), out.data_ptr(), _dtype_code(out_dtype),
             out.stride(0), out.stride(1),
             _stream(self._dev),
@@ -324,11 +331,14 @@ class HipBackend:
 
     def sdpa_prefill(
         self, qq: torch.Tensor, kk: torch.Tensor, vv: torch.Tensor, scale: float,
-        out_dtype: torch.dtype = torch.float32,
+        out_dtype: torch.dtype = torch.float32, q_offset: int = 0,
     ) -> torch.Tensor:
-        """Drop-in for prefill.py:60-68: (1, H, S, D), (1, Hkv, S, D) -> (1, H, S, D)."""
+        """Drop-in for the SDPA calls of prefill.py:60-68 (q_offset = 0) and
+        qwen36_moe.py:415-423 (q_offset = pos0, head-major cache views):
+        qq (1, H, S, D), kk/vv (1, Hkv, q_offset + S, D) -> (1, H, S, D)."""
         out = self.attention_prefill(
-            qq[0].transpose(0, 1), kk[0].transpose(0, 1), vv[0].transpose(0, 1), scale, out_dtype
+            qq[0].transpose(0, 1), kk[0].transpose(0, 1), vv[0].transpose(0, 1), scale, out_dtype,
+            q_offset=q_offset,
         )
         return out.transpose(0, 1).unsqueeze(0)
 

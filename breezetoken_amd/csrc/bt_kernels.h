@@ -56,7 +56,8 @@ struct PrefillParams {
   const uint16_t* v;
   int64_t q_stride_tok, q_stride_head;
   int64_t kv_stride_tok, kv_stride_head;
-  int32_t seqlen;
+  int32_t seqlen;      // new query rows S
+  int32_t q_offset;    // absolute position of query row 0 (keys: q_offset + S)
   int32_t heads;
   int32_t kv_heads;
   int32_t group;       // heads / kv_heads
@@ -69,10 +70,10 @@ struct PrefillParams {
 
 // Keys per block of the prefill key loop, and the size of the transposed fp16
 // V image the prefill builds in its workspace: per kv head and 64-key block,
-// 8 chunks of 8 keys x head_dim rows x 16 bytes.
+// 8 chunks of 8 keys x head_dim rows x 16 bytes, for kv_len keys.
 constexpr int kPrefillKeyBlock = 64;
-inline size_t prefill_vt_bytes(int seqlen, int kv_heads, int head_dim) {
-  const size_t blocks = (size_t)(seqlen + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
+inline size_t prefill_vt_bytes(int kv_len, int kv_heads, int head_dim) {
+  const size_t blocks = (size_t)(kv_len + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
   return (size_t)kv_heads * blocks * kPrefillKeyBlock * (size_t)head_dim * 2;
 }
 

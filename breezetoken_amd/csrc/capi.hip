@@ -253,18 +253,20 @@ int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, c
                                total_splits, out, out_dtype, out_stride_seq, stream);
 }
 
-int64_t bt_prefill_workspace_bytes(int32_t seqlen, int32_t kv_heads, int32_t head_dim) {
-  if (seqlen < 1 || kv_heads < 1 || head_dim < 1) return 0;
-  return (int64_t)bt::prefill_vt_bytes(seqlen, kv_heads, head_dim);
+int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
+  if (kv_len < 1 || kv_heads < 1 || head_dim < 1) return 0;
+  return (int64_t)bt::prefill_vt_bytes(kv_len, kv_heads, head_dim);
 }
 
 int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
                    int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
-                   int32_t seqlen, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
-                   void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
-                   int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+                   int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
+                   int32_t head_dim, float scale, void* workspace, int64_t workspace_bytes,
+                   void* out, int32_t out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
+                   void* stream) {
   if (!q || !k || !v || !out || !workspace) return BT_EINVAL;
-  if (seqlen < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads) return BT_EINVAL;
+  if (seqlen < 1 || q_offset < 0 || heads < 1 || kv_heads < 1 || heads % kv_heads) return BT_EINVAL;
+  if ((int64_t)q_offset + seqlen > INT32_MAX) return BT_EINVAL;
   if (out_dtype != BT_DTYPE_F32 && out_dtype != BT_DTYPE_BF16) return BT_EINVAL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return BT_EINVAL;
   if (q_stride_tok <= 0 || q_stride_head <= 0 || kv_stride_tok <= 0 || kv_stride_head < 0 ||
@@ -278,11 +280,12 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   if (heads / kv_heads > 8) return BT_ENOTSUP;
   // 32-bit buffer offsets: the K rows of one kv head (plus the last block's
   // tail) and its V^T image
-  const int64_t nblk = (seqlen + bt::kPrefillKeyBlock - 1) / bt::kPrefillKeyBlock;
+  const int32_t kv_len = q_offset + seqlen;
+  const int64_t nblk = ((int64_t)kv_len + bt::kPrefillKeyBlock - 1) / bt::kPrefillKeyBlock;
   if ((nblk + 1) * bt::kPrefillKeyBlock * kv_stride_tok * 2 > (int64_t)UINT32_MAX ||
       nblk * bt::kPrefillKeyBlock * head_dim * 2 > (int64_t)UINT32_MAX)
     return BT_ENOTSUP;
-  if (workspace_bytes < bt_prefill_workspace_bytes(seqlen, kv_heads, head_dim)) return BT_ENOSPC;
+  if (workspace_bytes < bt_prefill_workspace_bytes(kv_len, kv_heads, head_dim)) return BT_ENOSPC;
   bt::PrefillParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k);
@@ -292,6 +295,7 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   p.kv_stride_tok = kv_stride_tok;
   p.kv_stride_head = kv_stride_head;
   p.seqlen = seqlen;
+  p.q_offset = q_offset;
   p.heads = heads;
   p.kv_heads = kv_heads;
   p.group = heads / kv_heads;

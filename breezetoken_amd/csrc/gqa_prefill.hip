@@ -1,10 +1,13 @@
 // Causal GQA prefill attention for gfx950 (MI355X) on MFMA.
 //
-// Computes, for every query position i of a prompt that starts at slot 0 and
-// every query head h (kv head g = h / G),
-//     out[i, h] = softmax_j<=i (q_i . k_j * scale) . V_j
-// -- the F.scaled_dot_product_attention(is_causal=True, enable_gqa=True) call
-// of _prefill_attn (breezetoken/model/prefill.py:56-68).
+// Computes, for every new query row i (absolute position p0 + i, where p0 =
+// q_offset tokens are already in the cache) and every query head h (kv head
+// g = h / G),
+//     out[i, h] = softmax_{j <= p0+i} (q_i . k_j * scale) . V_j
+// over the p0 + S keys of the cache -- the F.scaled_dot_product_attention
+// (is_causal=True, enable_gqa=True) call of _prefill_attn (breezetoken/model/
+// prefill.py:56-68, p0 = 0) and the banded-mask chunked prefill of
+// Qwen36MoE._attn_batch (breezetoken/model/qwen36_moe.py:394-428).
 //
 // Decomposition (MI355X-first):
 //  * a small pre-pass writes V once per kv head as a transposed fp16 image
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(256) void prefill_vt_kernel(PrefillParams p) {
   const int nblk = gridDim.x;
   const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
   const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)p.seqlen * row_bytes);
+      make_rsrc(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)(p.q_offset + p.seqlen) * row_bytes);
   uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kKB * D;
   for (int item = threadIdx.x; item < 8 * kDC; item += 256) {
     const int c = item / kDC, dc = item % kDC;
@@ -181,22 +184,24 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
   const int G = p.group;
   const int GW = G < kWaves ? G : kWaves;
   const int pos_per_wg = kQB * (kWaves / GW);
-  const int S = p.seqlen;
+  const int S = p.seqlen;                 // new query rows
+  const int P0 = p.q_offset;              // absolute position of query row 0
+  const int nkeys = P0 + S;
   const int nqb = (S + pos_per_wg - 1) / pos_per_wg;
-  const int nblk = (S + kKB - 1) / kKB;
+  const int nblk = (nkeys + kKB - 1) / kKB;
   const int qblk = nqb - 1 - (int)blockIdx.x;  // heavy blocks first
   const int wg_q0 = qblk * pos_per_wg;
   const int q0 = wg_q0 + (wave / GW) * kQB;   // this wave's first position
   const int wg_qend = min(S, wg_q0 + pos_per_wg);
-  // keys needed by the work-group: [0, wg_qend)
-  const int nkb = (wg_qend + kKB - 1) / kKB;
+  // keys needed by the work-group: [0, P0 + wg_qend)
+  const int nkb = (P0 + wg_qend + kKB - 1) / kKB;
   const int last = nkb - 1;
 
   // Tile copies.  K copy i (1 KiB) is 16-byte chunk i of the 64 key rows, lane
   // l taking row l; V^T copy i is bytes [1024 i, +1024) of the block's image.
   // Wave w issues copies w, w + 4, ...
   const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)S * row_bytes);
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)nkeys * row_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.vt + (size_t)kvh * nblk * kKB * D, (uint32_t)nblk * kImg);
   const uint32_t k_voff = (uint32_t)lane * row_bytes;
   const uint32_t v_voff = (uint32_t)lane * 16;
@@ -259,7 +264,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       for (int j = 0; j < 16; ++j) oacc[i][j] = 0.f;
     float m_ref = -INFINITY;  // reference max (log2 domain) of this lane's column
     float l_run = 0.f;        // partial row sum over this lane's keys
-    const int my_q = q0 + qcol;
+    const int my_q = q0 + qcol;       // this lane's query row
+    const int my_pos = P0 + my_q;     // its absolute position: keys 0..my_pos
     // P of a key block as fp16 pairs: pk0 holds keys 0..31 of the block, pk1
     // keys 32..63 (the two 32-key halves of the S^T registers).
     uint32_t pk0[8], pk1[8];
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int key = key0 + mt * 32 + (j >> 2) * 8 + kgrp * 4 + (j & 3);
-          sacc[mt][j] = key <= my_q ? sacc[mt][j] : -INFINITY;
+          sacc[mt][j] = key <= my_pos ? sacc[mt][j] : -INFINITY;
         }
     };
     // exp2(s * c - m) of one 32-key half into fp16 pairs; returns the sum.
@@ -350,8 +356,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
         for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
       }
     };
-    // Blocks whose last key is <= q0 need no causal mask.
-    const int kb_diag = (q0 + 1) / kKB;
+    // Blocks whose last key is <= the wave's first position need no mask.
+    const int kb_diag = (P0 + q0 + 1) / kKB;
 
     // Copy schedule (double-buffered tiles, copies issued as soon as their
     // buffer is free, so each has about one and a half steps to land):
@@ -444,7 +450,7 @@ hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stre
   const int GW = G < kWaves ? G : kWaves;
   const int pos_per_wg = kQB * (kWaves / GW);
   const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
-  const int nblk = (p.seqlen + kKB - 1) / kKB;
+  const int nblk = (p.q_offset + p.seqlen + kKB - 1) / kKB;
   const dim3 grid(nqb, p.kv_heads), vt_grid(nblk, p.kv_heads);
   switch (head_dim) {
     case 128:

@@ -16,6 +16,11 @@ What each function restates, and what pins it (see ``tests/test_oracle.py``):
   call of ``_prefill_attn`` (breezetoken/model/prefill.py:56-78) and its
   einsum+tril fallback.  Pinned by: branch agreement, f64 brute force, row i ==
   decode over keys 0..i, row 0 == V[0].
+* ``torch_prefill_banded`` -- the explicit-band SDPA of the chunked prefill
+  ``Qwen36MoE._attn_batch`` (breezetoken/model/qwen36_moe.py:412-428).  Pinned
+  by: pos0 = 0 equals ``torch_prefill_attention``; rows pos0.. of a full
+  prefill equal the chunk; f64 brute force with an offset; a top-left-aligned
+  mask (``is_causal`` with S < seq) fails it.
 * ``split_partition`` / ``split_decode`` / ``combine_lse`` -- the split-KV
   partition, per-split log2-domain LSE + normalised partial, empty-split rule
   and LSE combine of ``gqa_decode`` (breezetoken/kernels/cuda/attention.py:

@@ -100,6 +100,28 @@ def torch_prefill_einsum(
     return out.permute(2, 0, 1, 3).reshape(steps, heads, dim)
 
 
+def torch_prefill_banded(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos0: int, scale: float
+) -> torch.Tensor:
+    """Chunked prefill with an explicit causal band, ``Qwen36MoE._attn_batch``
+    (qwen36_moe.py:412-428): q (S, H, D) are new tokens at absolute positions
+    pos0 .. pos0 + S - 1; k/v (pos0 + S, Hkv, D) the cache up to and including
+    them (token-major here; the reference reads the head-major view
+    ``k_cache[:, :seq]``, the same values).  Query row j sees keys 0 .. pos0 + j
+    (``k_idx <= q_idx``, qwen36_moe.py:414-417).  Returns (S, H, D) in f32.
+    """
+    steps = q.shape[0]
+    seq = pos0 + steps
+    k_idx = torch.arange(seq)
+    q_idx = pos0 + torch.arange(steps)
+    mask = k_idx.unsqueeze(0) <= q_idx.unsqueeze(1)  # (S, seq)
+    qq = q.float().transpose(0, 1).unsqueeze(0)
+    kk = k.float().transpose(0, 1).unsqueeze(0)
+    vv = v.float().transpose(0, 1).unsqueeze(0)
+    out = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=mask, scale=scale, enable_gqa=True)
+    return out[0].transpose(0, 1).contiguous()
+
+
 def fixed_decode(
     q: torch.Tensor, k_cap: torch.Tensor, v_cap: torch.Tensor, pos: int, scale: float
 ) -> torch.Tensor:
@@ -135,19 +157,23 @@ def brute_force_decode_f64(q, k, v, scale: float) -> np.ndarray:
     return out
 
 
-def brute_force_prefill_f64(q, k, v, scale: float) -> np.ndarray:
-    """Causal prefill in float64: row i is decode over keys 0..i. (S, H, D) -> (S, H, D)."""
+def brute_force_prefill_f64(q, k, v, scale: float, pos0: int = 0) -> np.ndarray:
+    """Causal prefill in float64: row i (position pos0 + i) is decode over keys
+    0..pos0+i.  q (S, H, D), k/v (pos0 + S, Hkv, D) -> (S, H, D)."""
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
     v = np.asarray(v, dtype=np.float64)
     steps, heads, dim = q.shape
     groups = k.shape[1]
     group = heads // groups
+    seq = k.shape[0]
+    assert seq == pos0 + steps
+    band = np.arange(seq)[None, :] <= (pos0 + np.arange(steps))[:, None]
     out = np.empty((steps, heads, dim), dtype=np.float64)
     for h in range(heads):
         g = h // group
-        s = (q[:, h, :] @ k[:, g, :].T) * scale  # (S, S)
-        s = np.where(np.tril(np.ones((steps, steps), dtype=bool)), s, -np.inf)
+        s = (q[:, h, :] @ k[:, g, :].T) * scale  # (S, seq)
+        s = np.where(band, s, -np.inf)
         s = s - s.max(axis=1, keepdims=True)
         p = np.exp(s)
         out[:, h, :] = (p @ v[:, g, :]) / p.sum(axis=1, keepdims=True)

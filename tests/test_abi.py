@@ -138,18 +138,22 @@ def test_entry_points_refuse_bad_arguments_before_launching():
     rc = lib.bt_gqa_decode_split(fake, 0, 0, fake, fake, 512, 256, None, None, None, 16, 1, 8, 2,
                                  256, 5000, 0.0625, fake, fake, None)
     assert rc == _lib.BT_ENOTSUP
-    # prefill: unserved head dim, bad strides, missing or short workspace
+    # prefill: unserved head dim, bad strides or offset, missing or short workspace
     big = 1 << 30
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 8, 2, 64, 0.125, fake, big,
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 0, 8, 2, 64, 0.125, fake, big,
                             fake, 0, 2048, 256, None)
     assert rc == _lib.BT_ENOTSUP
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 0, 8, 2, 256, 0.0625, fake, big,
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 0, 0, 8, 2, 256, 0.0625, fake, big,
                             fake, 0, 2048, 256, None)
     assert rc == _lib.BT_EINVAL
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 8, 2, 256, 0.0625, None, big,
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, -1, 8, 2, 256, 0.0625, fake, big,
                             fake, 0, 2048, 256, None)
     assert rc == _lib.BT_EINVAL
-    need = lib.bt_prefill_workspace_bytes(16, 2, 256)
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 8, 2, 256, 0.0625, fake,
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 0, 8, 2, 256, 0.0625, None, big,
+                            fake, 0, 2048, 256, None)
+    assert rc == _lib.BT_EINVAL
+    # the V^T workspace covers q_offset + seqlen keys
+    need = lib.bt_prefill_workspace_bytes(16 + 100, 2, 256)
+    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 100, 8, 2, 256, 0.0625, fake,
                             need - 1, fake, 0, 2048, 256, None)
     assert rc == _lib.BT_ENOSPC

@@ -242,3 +242,23 @@ def test_unserved_shapes_raise(hip_backend):
         hip_backend.attention(torch.randn(8, 96, device="cuda"),
                               torch.zeros(4, 2, 96, dtype=torch.bfloat16, device="cuda"),
                               torch.zeros(4, 2, 96, dtype=torch.bfloat16, device="cuda"), 0.1)
+
+
+@pytest.mark.parametrize("seq", [1, 33, 1000, 8192])
+def test_head_major_cache_decode(hip_backend, seq):
+    """The decode SDPA of qwen36_moe.py:444-455 on a head-major (Hkv, cap, D)
+    cache: the (S, Hkv, D) views k_cache[:, :seq].transpose(0, 1) are read in
+    place (token stride D, head stride cap*D), eagerly and with a device pos."""
+    cap = 8192
+    g = torch.Generator().manual_seed(seq + 77)
+    q = torch.randn(16, 256, generator=g)
+    kc = torch.randn(2, cap, 256, generator=g).to(torch.bfloat16)
+    vc = torch.randn(2, cap, 256, generator=g).to(torch.bfloat16)
+    scale = 256**-0.5
+    print(f"[head-major] seq={seq}", flush=True)
+    ref = orc.torch_attention(q, kc[:, :seq].transpose(0, 1).float(), vc[:, :seq].transpose(0, 1).float(), scale)
+    qd, kd, vd = _dev(q, kc, vc)
+    out = hip_backend.attention(qd, kd[:, :seq].transpose(0, 1), vd[:, :seq].transpose(0, 1), scale)
+    assert_close(out, ref)
+    pos = torch.tensor([seq - 1], dtype=torch.int32, device="cuda")
+    assert_close(hip_backend.attention_fixed(qd, kd.transpose(0, 1), vd.transpose(0, 1), pos, scale), ref)

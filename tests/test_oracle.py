@@ -230,6 +230,47 @@ def test_prefill_row_i_is_decode_over_prefix():
         assert torch.allclose(out[0, h], v[0, h // group], atol=1e-6)
 
 
+# ----------------------------------------------------------- chunked prefill
+@pytest.mark.parametrize("pos0,steps", [(0, 40), (5, 1), (17, 23), (64, 64), (100, 7)])
+def test_banded_prefill_matches_f64_with_offset(pos0, steps):
+    q, k, v = _prefill_inputs(pos0 + steps, seed=pos0 * 7 + steps)
+    out = orc.torch_prefill_banded(q[pos0:], k, v, pos0, SCALE)
+    ref = orc.brute_force_prefill_f64(q[pos0:].numpy(), k.numpy(), v.numpy(), SCALE, pos0=pos0)
+    assert out.shape == (steps, H, D)
+    assert orc.compare(out.numpy(), ref)[0] < 1e-5
+
+
+def test_banded_prefill_zero_offset_is_causal_prefill():
+    q, k, v = _prefill_inputs(50, seed=21)
+    a = orc.torch_prefill_banded(q, k, v, 0, SCALE)
+    b = orc.torch_prefill_attention(q, k, v, SCALE)
+    assert (a - b).abs().max().item() < 2e-6
+
+
+def test_chunked_prefill_equals_full_prefill_rows():
+    """Prefilling [0, 96) at once and prefilling [40, 96) after [0, 40) give the
+    same rows for positions 40..95 (qwen36_moe.py:394-428 vs prefill.py:56-68)."""
+    q, k, v = _prefill_inputs(96, seed=22)
+    full = orc.torch_prefill_attention(q, k, v, SCALE)
+    chunk = orc.torch_prefill_banded(q[40:], k, v, 40, SCALE)
+    assert (full[40:] - chunk).abs().max().item() < 2e-6
+
+
+def test_planted_top_left_mask_for_chunk_is_caught():
+    """``is_causal=True`` with S < seq aligns the mask top-left (row j sees keys
+    0..j), which is what the reference's explicit band avoids
+    (qwen36_moe.py:412-413); that mistake fails the f64 check."""
+    q, k, v = _prefill_inputs(60, seed=23)
+    pos0 = 36
+    ref = orc.brute_force_prefill_f64(q[pos0:].numpy(), k.numpy(), v.numpy(), SCALE, pos0=pos0)
+    qq = q[pos0:].transpose(0, 1).unsqueeze(0)
+    kk = k.transpose(0, 1).unsqueeze(0)
+    vv = v.transpose(0, 1).unsqueeze(0)
+    bad = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, is_causal=True, scale=SCALE,
+                                                           enable_gqa=True)
+    assert orc.compare(bad[0].transpose(0, 1).numpy(), ref)[0] > 1e-2
+
+
 def test_planted_wrong_causal_diagonal_is_caught():
     """Masking j < i (excluding the diagonal) instead of j <= i fails the f64 check."""
     q, k, v = _prefill_inputs(24, seed=16)

@@ -119,3 +119,53 @@ def test_prefill_unserved_raises(hip_backend):
     q, k, v, scale = _inputs(16, dim=64)
     with pytest.raises(RuntimeError):
         hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale)
+
+
+# ---------------------------------------------- chunked prefill (query offset)
+@pytest.mark.parametrize("steps,pos0", [(128, 17), (300, 1000), (64, 64), (1, 5000), (65, 63), (257, 4096)])
+def test_chunked_prefill_query_offset(hip_backend, steps, pos0):
+    """The banded-mask chunk of qwen36_moe.py:394-428: queries at positions
+    pos0 .. pos0 + S - 1 over keys 0 .. pos0 + S - 1."""
+    g = torch.Generator().manual_seed(steps * 31 + pos0)
+    q = torch.randn(steps, 16, 256, generator=g).to(torch.bfloat16)
+    k = torch.randn(pos0 + steps, 2, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(pos0 + steps, 2, 256, generator=g).to(torch.bfloat16)
+    scale = 256**-0.5
+    print(f"[chunk] S={steps} pos0={pos0}", flush=True)
+    ref = orc.torch_prefill_banded(q.float(), k.float(), v.float(), pos0, scale)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, q_offset=pos0)
+    assert out.shape == (steps, 16, 256)
+    _close(out, ref)
+
+
+def test_chunked_prefill_head_major_cache(hip_backend):
+    """The SDPA call of qwen36_moe.py:415-423 on views of a head-major
+    (Hkv, capacity, D) cache, and the chunks together equal one full prefill."""
+    cap, total, split = 4096, 900, 333
+    g = torch.Generator().manual_seed(40)
+    kc = torch.zeros(2, cap, 256, dtype=torch.bfloat16)
+    vc = torch.zeros(2, cap, 256, dtype=torch.bfloat16)
+    kc[:, :total] = torch.randn(2, total, 256, generator=g).to(torch.bfloat16)
+    vc[:, :total] = torch.randn(2, total, 256, generator=g).to(torch.bfloat16)
+    q = torch.randn(total, 8, 256, generator=g).to(torch.bfloat16)
+    scale = 256**-0.5
+    kd, vd, qd = kc.cuda(), vc.cuda(), q.cuda()
+    full = hip_backend.attention_prefill(qd, kd[:, :total].transpose(0, 1), vd[:, :total].transpose(0, 1), scale)
+    parts = []
+    for lo, hi in ((0, split), (split, total)):
+        qq = qd[lo:hi].transpose(0, 1).unsqueeze(0)
+        out = hip_backend.sdpa_prefill(qq, kd[:, :hi].unsqueeze(0), vd[:, :hi].unsqueeze(0), scale, q_offset=lo)
+        assert out.shape == (1, 8, hi - lo, 256)
+        parts.append(out[0].transpose(0, 1))
+    chunked = torch.cat(parts)
+    ref = orc.torch_prefill_attention(q.float(), kc[:, :total].transpose(0, 1).float(),
+                                      vc[:, :total].transpose(0, 1).float(), scale)
+    _close(chunked, ref)
+    _close(full, ref)
+    assert (chunked - full).abs().max().item() <= 1e-3
+
+
+def test_chunked_prefill_bad_offset_raises(hip_backend):
+    q, k, v, scale = _inputs(16)
+    with pytest.raises(RuntimeError):
+        hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, q_offset=3)
