@@ -109,7 +109,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
   static_assert(kVLoads >= 1, "V tile must fill at least one wave load");
 
   // LDS: one V tile per wave; reused for the cross-wave merge at the end.
-  constexpr int kMergeBytes = WAVES * GMAX * (D + 2) * 4;
+  // Merge rows [wave][head][d] have a stride of D + 4 floats (= 4 banks mod
+  // 64), so the lanes that write one d-tile of different heads fall on
+  // distinct bank groups instead of conflicting on a 1 KiB row stride.
+  constexpr int kMoStride = D + 4;
+  constexpr int kMergeBytes = WAVES * GMAX * (kMoStride + 2) * 4;
   constexpr int kVBytes = WAVES * kVTileBytes;
   constexpr int kLdsBytes = kVBytes > kMergeBytes ? kVBytes : kMergeBytes;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kLdsBytes];
@@ -444,19 +448,26 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
 
   // ---- cross-wave merge through LDS ----------------------------------------
   __syncthreads();  // every wave is done with its V tile
-  float* mo = reinterpret_cast<float*>(smem);              // [wave][GMAX][D]
-  float* mm = mo + WAVES * GMAX * D;                        // [wave][GMAX]
+  float* mo = reinterpret_cast<float*>(smem);              // [wave][GMAX][kMoStride]
+  float* mm = mo + WAVES * GMAX * kMoStride;                // [wave][GMAX]
   float* ml = mm + WAVES * GMAX;                            // [wave][GMAX]
-  if (col < G && !col_lo) {
-    float* dst = mo + (wave * GMAX + col) * D;
+  // After the mirror sum, the hi lane (col = h) and the lo lane (col =
+  // 2*GMAX-1-h) hold the same head-h sums: the hi lane stores the even
+  // d-tiles and the lo lane the odd ones, so each store instruction carries
+  // twice the lanes and a wave issues kDTiles/2 of them.  When all waves of
+  // the group reach this point together, LDS store throughput is the cost.
+  if (col_head >= 0 && col_head < G) {
+    const int par = col_lo ? 1 : 0;
+    float* dst = mo + (wave * GMAX + col_head) * kMoStride + par * 16 + kg * 4;
 #pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) {
-      float4 v4 = {oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]};
-      *reinterpret_cast<float4*>(dst + dt * 16 + kg * 4) = v4;
+    for (int q = 0; q < kDTiles / 2; ++q) {
+      const floatx4 a = oacc[2 * q], b = oacc[2 * q + 1];
+      const float4 v4 = {par ? b[0] : a[0], par ? b[1] : a[1], par ? b[2] : a[2], par ? b[3] : a[3]};
+      *reinterpret_cast<float4*>(dst + q * 32) = v4;
     }
-    if (kg == 0) {
-      mm[wave * GMAX + col] = m_run;
-      ml[wave * GMAX + col] = l_run;
+    if (kg == 0 && !col_lo) {
+      mm[wave * GMAX + col_head] = m_run;
+      ml[wave * GMAX + col_head] = l_run;
     }
   }
   __syncthreads();
@@ -476,7 +487,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
       if (lw > 0.f) {
         const float sc = fast_exp2(mm[w * GMAX + h] - mx);
         lsum += lw * sc;
-        const float4 o = *reinterpret_cast<const float4*>(mo + (w * GMAX + h) * D + d);
+        const float4 o = *reinterpret_cast<const float4*>(mo + (w * GMAX + h) * kMoStride + d);
         acc.x += o.x * sc; acc.y += o.y * sc; acc.z += o.z * sc; acc.w += o.w * sc;
       }
     }
