@@ -60,6 +60,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
          _c_f32, _vp, _c_i64, _vp, _c_i32, _c_i64, _c_i64, _vp],
     ),
+    "bt_rms_norm_rope": (
+        ctypes.c_int,
+        [_vp, _c_i64, _c_i32, _c_i32, _vp, _c_f32, _vp, _vp, _vp, _c_i32, _c_i32, _vp, _c_i64, _vp],
+    ),
+    "bt_attn_prep": (
+        ctypes.c_int,
+        [_vp, _c_i32, _c_i32, _c_i32, _vp, _vp, _c_f32, _vp, _vp, _vp, _c_i32, _c_i32, _vp, _c_i32,
+         _vp, _vp, _c_i64, _c_i64, _c_i32, _vp],
+    ),
 }
 
 _lock = threading.Lock()

@@ -17,7 +17,12 @@ and adds the operators the reference runs outside the protocol:
   (S, H, D) (the SDPA call of prefill.py:56-68, and with q_offset > 0 the
   banded chunked prefill of qwen36_moe.py:394-428); ``sdpa_prefill`` takes
   those calls' (1, H, S, D) layout;
-* ``attention_ragged(...)``: many sequences in one shared cache.
+* ``attention_ragged(...)``: many sequences in one shared cache;
+* ``rms_norm(x, w, eps)`` and ``rope(x, cos, sin, pos, rope_dim)``: the
+  reference Backend's q/k norm and partial RoPE operators (backends.py:44-62);
+* ``attn_prep(...)``: the whole decode-step preparation of an attention layer
+  (q/k RMSNorm + RoPE, bf16 cache writes at the device position) in one launch
+  (layers.py:58-73, graph.py:41-53).
 
 Every launch goes through libbreezetoken_amd.so on torch's current stream with
 no host synchronisation, so the calls can be captured in a hipGraph
@@ -37,6 +42,7 @@ from . import _lib
 from ._lib import BT_DTYPE_BF16, BT_DTYPE_F32, check
 
 SERVED_HEAD_DIMS = (64, 128, 256)
+SERVED_PREP_DIMS = (64, 128, 256, 512)
 SERVED_PREFILL_HEAD_DIMS = (128, 256)
 MAX_GROUP = 8
 
@@ -341,6 +347,120 @@ class HipBackend:
             q_offset=q_offset,
         )
         return out.transpose(0, 1).unsqueeze(0)
+
+    # ------------------------------------------ q/k norm, RoPE and cache writes
+    def _check_f32_dev(self, name: str, t: torch.Tensor) -> None:
+        if t.dtype != torch.float32:
+            raise RuntimeError(f"{name} must be f32 (the reference keeps activations in f32)")
+        if t.device != self._dev:
+            raise RuntimeError(f"{name} must live on the backend's device")
+
+    def _rope_args(self, cos, sin, pos, rope_dim: int):
+        if cos is None:
+            return None, None, None, 0, 1
+        for n, t in (("cos", cos), ("sin", sin)):
+            self._check_f32_dev(n, t)
+            if t.ndim != 2 or t.shape[1] != rope_dim or not t.is_contiguous():
+                raise RuntimeError(f"{n} must be a contiguous (cap, rope_dim) table")
+        if sin.shape != cos.shape:
+            raise RuntimeError("cos and sin tables differ in shape")
+        if pos.dtype != torch.int32:
+            pos = pos.reshape(-1).to(torch.int32)
+        if pos.device != self._dev:
+            raise RuntimeError("pos must be a device tensor")
+        return cos, sin, pos.reshape(-1)[:1], int(rope_dim), int(cos.shape[0])
+
+    def _rows(self, x, w, eps, cos, sin, pos, rope_dim) -> torch.Tensor:
+        self._check_f32_dev("x", x)
+        dim = x.shape[-1]
+        if dim not in SERVED_PREP_DIMS:
+            raise RuntimeError(f"row length {dim} is not served {SERVED_PREP_DIMS}")
+        rows = x.numel() // dim
+        xr = x.reshape(rows, dim).contiguous()
+        out = torch.empty_like(xr)
+        if w is not None:
+            self._check_f32_dev("w", w)
+            w = w.reshape(-1).contiguous()
+        cos, sin, pos, rope_dim, cap = self._rope_args(cos, sin, pos, rope_dim)
+        rc = self._lib.bt_rms_norm_rope(
+            xr.data_ptr(), dim, rows, dim, _ptr(w), float(eps), _ptr(cos), _ptr(sin), _ptr(pos),
+            rope_dim, cap, out.data_ptr(), dim, _stream(self._dev),
+        )
+        check("bt_rms_norm_rope", rc)
+        return out.reshape(x.shape)
+
+    def rms_norm(self, x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+        """RMSNorm over the last dimension with a flat learned weight:
+        x * rsqrt(mean(x^2) + eps) * w in f32 (backends.py:44-45, 187-189)."""
+        if x.shape[-1] != w.numel():
+            raise ValueError(f"rms_norm shape mismatch: x {tuple(x.shape)}, w {tuple(w.shape)}")
+        return self._rows(x, w, eps, None, None, None, 0)
+
+    def rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
+             rope_dim: int) -> torch.Tensor:
+        """Partial rotate-half RoPE on the leading ``rope_dim`` dimensions at the
+        device position ``pos`` (backends.py:54-62, 218-226)."""
+        if rope_dim < 2 or rope_dim % 2 or rope_dim > x.shape[-1]:
+            raise ValueError(f"invalid rope_dim {rope_dim} for rows of {x.shape[-1]}")
+        return self._rows(x, None, 0.0, cos, sin, pos, rope_dim)
+
+    @staticmethod
+    def _cache_strides(cache: torch.Tensor, kv_heads: int, dim: int) -> tuple[int, int, int]:
+        if cache.dtype != torch.bfloat16 or cache.stride(-1) != 1:
+            raise RuntimeError("the cache must be bf16 with unit d-stride")
+        if cache.ndim == 2 and cache.shape[1] == kv_heads * dim:
+            return cache.shape[0], cache.stride(0), dim
+        if cache.ndim == 3 and cache.shape[1:] == (kv_heads, dim):
+            return cache.shape[0], cache.stride(0), cache.stride(1)
+        raise RuntimeError("the cache must be (cap, Hkv*D) or a (cap, Hkv, D) view")
+
+    def attn_prep(
+        self, qkv: torch.Tensor, q_norm: torch.Tensor | None, k_norm: torch.Tensor | None,
+        eps: float, cos: torch.Tensor | None, sin: torch.Tensor | None, pos: torch.Tensor,
+        rope_dim: int, cache_k: torch.Tensor, cache_v: torch.Tensor, heads: int, kv_heads: int,
+        head_dim: int, q_dtype: torch.dtype = torch.float32,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Decode-step preparation of one attention layer (layers.py:58-73,
+        graph.py:41-53) in one launch: from the fused projection output ``qkv``
+        ([H x (q | gate) | Hkv x k | Hkv x v], f32) write k = rope(rms_norm(k))
+        and v into the bf16 caches at slot ``pos`` (device int32) and return
+        (q, gate): q = rope(rms_norm(q)) (H, D) in ``q_dtype`` and the gate as
+        an (H, D) view of ``qkv``."""
+        self._check_f32_dev("qkv", qkv)
+        D = int(head_dim)
+        if qkv.numel() != heads * 2 * D + 2 * kv_heads * D or heads % kv_heads:
+            raise RuntimeError("qkv does not hold H x (q | gate) + 2 x Hkv x D values")
+        if D not in SERVED_PREP_DIMS:
+            raise RuntimeError(f"head_dim {D} is not served {SERVED_PREP_DIMS}")
+        qkv = qkv.reshape(-1).contiguous()
+        if (q_norm is None) != (k_norm is None):
+            raise RuntimeError("q_norm and k_norm are given together")
+        if q_norm is not None:
+            self._check_f32_dev("q_norm", q_norm)
+            self._check_f32_dev("k_norm", k_norm)
+            if q_norm.numel() != D or k_norm.numel() != D:
+                raise ValueError("q_norm/k_norm must hold head_dim values")
+            q_norm, k_norm = q_norm.reshape(-1).contiguous(), k_norm.reshape(-1).contiguous()
+        cos, sin, pos_d, rope_dim, rcap = self._rope_args(cos, sin, pos, rope_dim)
+        if pos_d is None:
+            pos_d = pos.reshape(-1)[:1]
+            if pos_d.dtype != torch.int32 or pos_d.device != self._dev:
+                raise RuntimeError("pos must be a device int32 tensor")
+        cap, st_tok, st_head = self._cache_strides(cache_k, kv_heads, D)
+        if self._cache_strides(cache_v, kv_heads, D) != (cap, st_tok, st_head):
+            raise RuntimeError("k and v caches need identical shapes and strides")
+        for n, t in (("cache_k", cache_k), ("cache_v", cache_v)):
+            if t.device != self._dev:
+                raise RuntimeError(f"{n} must live on the backend's device")
+        q = torch.empty((heads, D), dtype=q_dtype, device=self._dev)
+        rc = self._lib.bt_attn_prep(
+            qkv.data_ptr(), heads, kv_heads, D, _ptr(q_norm), _ptr(k_norm), float(eps), _ptr(cos),
+            _ptr(sin), pos_d.data_ptr(), rope_dim, rcap, q.data_ptr(), _dtype_code(q_dtype),
+            cache_k.data_ptr(), cache_v.data_ptr(), st_tok, st_head, cap, _stream(self._dev),
+        )
+        check("bt_attn_prep", rc)
+        gate = qkv[: heads * 2 * D].view(heads, 2 * D)[:, D:]
+        return q, gate
 
     def close(self) -> None:
         self._ws.clear()

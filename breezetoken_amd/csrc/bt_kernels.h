@@ -68,6 +68,33 @@ struct PrefillParams {
   uint16_t* vt;        // workspace: fp16 V^T image, prefill_vt_bytes() bytes
 };
 
+// Per-row RMSNorm + RoPE (row mode) and the fused decode-step preparation
+// (attention mode); see attn_prep.hip.
+struct RowPrepParams {
+  const float* x;            // row mode: (rows, D) rows; attention mode: the fused projection output
+  int64_t x_stride;          // row mode: elements between rows
+  int32_t rows;              // row mode
+  float* out;                // row mode: (rows, D) f32
+  int64_t out_stride;
+  const float* w;            // RMSNorm weight (D,) (q weight in attention mode), or null: no norm
+  const float* wk;           // attention mode: k RMSNorm weight (D,), or null
+  float eps;
+  const float* cos;          // (rope_cap, rope_dim) tables, or null: no rotation
+  const float* sin;
+  const int32_t* pos;        // device position (1,)
+  int32_t rope_dim;
+  int32_t rope_cap;
+  int32_t heads;             // attention mode
+  int32_t kv_heads;
+  void* q_out;               // (heads, D) f32 or bf16
+  int q_out_bf16;
+  uint16_t* cache_k;         // bf16 cache, token-major slots
+  uint16_t* cache_v;
+  int64_t kv_stride_tok;
+  int64_t kv_stride_head;
+  int32_t cache_cap;
+};
+
 // Keys per block of the prefill key loop, and the size of the transposed fp16
 // V image the prefill builds in its workspace: per kv head and 64-key block,
 // 8 chunks of 8 keys x head_dim rows x 16 bytes, for kv_len keys.
@@ -100,5 +127,7 @@ hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int gri
 hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads, int batch,
                                  hipStream_t stream);
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stream);
+hipError_t launch_row_norm_rope(const RowPrepParams& p, int head_dim, hipStream_t stream);
+hipError_t launch_attn_prep(const RowPrepParams& p, int head_dim, hipStream_t stream);
 
 }  // namespace bt

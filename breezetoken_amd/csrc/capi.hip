@@ -308,4 +308,68 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   return hip_rc(bt::launch_prefill(p, head_dim, (hipStream_t)stream));
 }
 
+static bool prep_dim_served(int32_t d) { return d == 64 || d == 128 || d == 256 || d == 512; }
+
+int bt_rms_norm_rope(const float* x, int64_t x_stride, int32_t rows, int32_t dim, const float* w,
+                     float eps, const float* cos, const float* sin, const int32_t* pos,
+                     int32_t rope_dim, int32_t rope_cap, float* out, int64_t out_stride,
+                     void* stream) {
+  if (!x || !out || rows < 1 || dim < 1 || x_stride < dim || out_stride < dim) return BT_EINVAL;
+  if ((cos == nullptr) != (sin == nullptr)) return BT_EINVAL;
+  if (cos && (!pos || rope_dim < 2 || rope_dim % 2 || rope_dim > dim || rope_cap < 1)) return BT_EINVAL;
+  if (!w && !cos) return BT_EINVAL;
+  if (!(eps >= 0.f)) return BT_EINVAL;
+  if (!prep_dim_served(dim)) return BT_ENOTSUP;
+  bt::RowPrepParams p{};
+  p.x = x;
+  p.x_stride = x_stride;
+  p.rows = rows;
+  p.out = out;
+  p.out_stride = out_stride;
+  p.w = w;
+  p.eps = eps;
+  p.cos = cos;
+  p.sin = sin;
+  p.pos = pos;
+  p.rope_dim = cos ? rope_dim : 0;
+  p.rope_cap = rope_cap;
+  return hip_rc(bt::launch_row_norm_rope(p, dim, (hipStream_t)stream));
+}
+
+int bt_attn_prep(const float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                 const float* q_norm, const float* k_norm, float eps, const float* cos,
+                 const float* sin, const int32_t* pos, int32_t rope_dim, int32_t rope_cap,
+                 void* q_out, int32_t q_dtype, void* cache_k, void* cache_v, int64_t kv_stride_tok,
+                 int64_t kv_stride_head, int32_t cache_cap, void* stream) {
+  if (!qkv || !pos || !q_out || !cache_k || !cache_v) return BT_EINVAL;
+  if (heads < 1 || kv_heads < 1 || head_dim < 1 || cache_cap < 1) return BT_EINVAL;
+  if ((q_norm == nullptr) != (k_norm == nullptr)) return BT_EINVAL;
+  if ((cos == nullptr) != (sin == nullptr)) return BT_EINVAL;
+  if (cos && (rope_dim < 2 || rope_dim % 2 || rope_dim > head_dim || rope_cap < 1)) return BT_EINVAL;
+  if (q_dtype != BT_DTYPE_F32 && q_dtype != BT_DTYPE_BF16) return BT_EINVAL;
+  if (kv_stride_tok < 1 || kv_stride_head < 1) return BT_EINVAL;
+  if (!(eps >= 0.f)) return BT_EINVAL;
+  if (!prep_dim_served(head_dim)) return BT_ENOTSUP;
+  bt::RowPrepParams p{};
+  p.x = qkv;
+  p.w = q_norm;
+  p.wk = k_norm;
+  p.eps = eps;
+  p.cos = cos;
+  p.sin = sin;
+  p.pos = pos;
+  p.rope_dim = cos ? rope_dim : 0;
+  p.rope_cap = rope_cap;
+  p.heads = heads;
+  p.kv_heads = kv_heads;
+  p.q_out = q_out;
+  p.q_out_bf16 = q_dtype == BT_DTYPE_BF16;
+  p.cache_k = static_cast<uint16_t*>(cache_k);
+  p.cache_v = static_cast<uint16_t*>(cache_v);
+  p.kv_stride_tok = kv_stride_tok;
+  p.kv_stride_head = kv_stride_head;
+  p.cache_cap = cache_cap;
+  return hip_rc(bt::launch_attn_prep(p, head_dim, (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -147,6 +147,39 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
                    void* out, int32_t out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
                    void* stream);
 
+/* Per-row RMSNorm and/or partial rotate-half RoPE over rows of f32.  Replaces
+ * Backend.rms_norm (breezetoken/backends.py:44-45; torch form 187-189:
+ * x * rsqrt(mean(x^2) + eps) * w) and Backend.rope (backends.py:54-62; torch
+ * form 218-226, kernel kernels/cuda/rope.py:13-43) on a (rows, dim) view:
+ * x (rows, dim) with row stride x_stride -> out (rows, dim), row stride
+ * out_stride (out may equal x).  w (dim,) or NULL: no norm (applied first).
+ * cos/sin (rope_cap, rope_dim) tables or both NULL: no rotation; the first
+ * rope_dim (even) dims of each row turn by row *pos of the tables, the rest
+ * pass through; a position outside [0, rope_cap) uses the nearest row.
+ * dim in {64, 128, 256, 512}. */
+int bt_rms_norm_rope(const float* x, int64_t x_stride, int32_t rows, int32_t dim, const float* w,
+                     float eps, const float* cos, const float* sin, const int32_t* pos,
+                     int32_t rope_dim, int32_t rope_cap, float* out, int64_t out_stride,
+                     void* stream);
+
+/* Fused decode-step preparation of one attention layer, in one launch.
+ * Replaces the q/k RMSNorm + RoPE calls and the two cache writes of
+ * LayerMixin._attn (breezetoken/model/layers.py:58-73) and
+ * GraphMixin._graph_attn (breezetoken/model/graph.py:41-53): qkv is the fused
+ * projection output laid out as in layers.py:58-64, [heads x (q | gate) of
+ * 2*head_dim | kv_heads x k of head_dim | kv_heads x v of head_dim] f32.
+ * Writes q_out (heads, head_dim) = rope(rms_norm(q, q_norm)) as f32 or bf16
+ * (q_dtype), and at slot *pos of the bf16 cache (element (slot, kv_head, d) at
+ * slot*kv_stride_tok + kv_head*kv_stride_head + d, token-major or head-major)
+ * k = rope(rms_norm(k, k_norm)) and v, rounded to bf16.  q_norm/k_norm both
+ * set or both NULL; cos/sin as in bt_rms_norm_rope.  A position outside
+ * [0, cache_cap) writes no cache slot.  The gate half of qkv is not touched. */
+int bt_attn_prep(const float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                 const float* q_norm, const float* k_norm, float eps, const float* cos,
+                 const float* sin, const int32_t* pos, int32_t rope_dim, int32_t rope_cap,
+                 void* q_out, int32_t q_dtype, void* cache_k, void* cache_v, int64_t kv_stride_tok,
+                 int64_t kv_stride_head, int32_t cache_cap, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

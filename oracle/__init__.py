@@ -35,4 +35,15 @@ What each function restates, and what pins it (see ``tests/test_oracle.py``):
   prefix, invariance to garbage written past ``pos``.
 * ``brute_force_decode_f64`` / ``brute_force_prefill_f64`` -- float64 numpy
   restatements of the attention definition, checked against closed forms.
+* ``prep.torch_rms_norm`` / ``prep.torch_rope`` / ``prep.rope_tables`` /
+  ``prep.attn_prep`` -- the q/k RMSNorm (breezetoken/backends.py:187-189),
+  partial rotate-half RoPE (backends.py:218-226), its cos/sin tables
+  (breezetoken/model/layers.py:26-32) and the decode-step preparation of an
+  attention layer (layers.py:58-73).  Pinned by (``tests/test_oracle_prep.py``):
+  float64 loops in the reference kernel's partner/sign form
+  (kernels/cuda/rope.py:31-37) on the reference test's random tables, closed
+  forms (constant rows, scale invariance, table angles), rotation properties
+  (identity at 0, pair norms, composition), planted mistakes (sum for mean,
+  missing weight or eps, flipped sign, interleaved pairs, wrong table row) and
+  segment markers for the projection slicing.
 """

@@ -157,3 +157,37 @@ def test_entry_points_refuse_bad_arguments_before_launching():
     rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 100, 8, 2, 256, 0.0625, fake,
                             need - 1, fake, 0, 2048, 256, None)
     assert rc == _lib.BT_ENOSPC
+
+
+def test_norm_rope_and_prep_refuse_bad_arguments_before_launching():
+    """bt_rms_norm_rope / bt_attn_prep validation happens on the host."""
+    lib = _lib.lib()
+    fake = 1 << 20
+    # rms_norm_rope: null x, nothing to do, odd or oversized rope_dim, cos without sin, unserved dim
+    assert lib.bt_rms_norm_rope(None, 256, 4, 256, fake, 1e-6, None, None, None, 0, 1, fake, 256,
+                                None) == _lib.BT_EINVAL
+    assert lib.bt_rms_norm_rope(fake, 256, 4, 256, None, 1e-6, None, None, None, 0, 1, fake, 256,
+                                None) == _lib.BT_EINVAL
+    assert lib.bt_rms_norm_rope(fake, 256, 4, 256, None, 0.0, fake, fake, fake, 63, 16, fake, 256,
+                                None) == _lib.BT_EINVAL
+    assert lib.bt_rms_norm_rope(fake, 256, 4, 256, None, 0.0, fake, fake, fake, 258, 16, fake, 256,
+                                None) == _lib.BT_EINVAL
+    assert lib.bt_rms_norm_rope(fake, 256, 4, 256, None, 0.0, fake, None, fake, 64, 16, fake, 256,
+                                None) == _lib.BT_EINVAL
+    assert lib.bt_rms_norm_rope(fake, 256, 4, 256, fake, -1.0, None, None, None, 0, 1, fake, 256,
+                                None) == _lib.BT_EINVAL
+    assert lib.bt_rms_norm_rope(fake, 96, 4, 96, fake, 1e-6, None, None, None, 0, 1, fake, 96,
+                                None) == _lib.BT_ENOTSUP
+    # attn_prep: null pos, one norm weight only, bad q dtype, unserved head_dim
+    args = [fake, 8, 2, 256, fake, fake, 1e-6, fake, fake, fake, 64, 4096, fake, 0, fake, fake, 512,
+            256, 65536, None]
+    bad = list(args); bad[9] = None
+    assert lib.bt_attn_prep(*bad) == _lib.BT_EINVAL
+    bad = list(args); bad[5] = None
+    assert lib.bt_attn_prep(*bad) == _lib.BT_EINVAL
+    bad = list(args); bad[13] = 7
+    assert lib.bt_attn_prep(*bad) == _lib.BT_EINVAL
+    bad = list(args); bad[10] = 65
+    assert lib.bt_attn_prep(*bad) == _lib.BT_EINVAL
+    bad = list(args); bad[3] = 80; bad[10] = 64
+    assert lib.bt_attn_prep(*bad) == _lib.BT_ENOTSUP
