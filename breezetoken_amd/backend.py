@@ -47,6 +47,17 @@ SERVED_PREFILL_HEAD_DIMS = (128, 256)
 MAX_GROUP = 8
 
 
+def rope_tables(cap: int, rope_dim: int, theta: float, device: str | torch.device = "cuda"):
+    """cos/sin (cap, rope_dim) f32 tables for ``rope``/``attn_prep``, built as
+    LayerMixin._rope_tables does (layers.py:26-32): inverse frequencies
+    theta^(-i/half), phases position * inverse frequency, both halves equal."""
+    half = rope_dim // 2
+    inv = theta ** (-torch.arange(0, half, device=device, dtype=torch.float32) / half)
+    phases = torch.outer(torch.arange(cap, device=device, dtype=torch.float32), inv)
+    freqs = torch.cat((phases, phases), dim=-1)
+    return freqs.cos(), freqs.sin()
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 

@@ -74,10 +74,18 @@ def _rope(x, pos):
     return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)
 
 
+def _rope_tab(x, positions, cos, sin):
+    """The same rotation from (CAP, D) tables (layers.py:26-32, backends.py:218-226)."""
+    half = D // 2
+    c, s_ = cos[positions][:, None, :], sin[positions][:, None, :]
+    return x * c + torch.cat((-x[..., half:], x[..., :half]), dim=-1) * s_
+
+
 class _Decoder:
-    def __init__(self, params, attn_prefill, attn_decode, device):
+    def __init__(self, params, attn_prefill, attn_decode, device, tables=None, prep_decode=None):
         self.layers, self.emb, self.head, _ = params
         self.attn_prefill, self.attn_decode = attn_prefill, attn_decode
+        self.tables, self.prep_decode = tables, prep_decode
         self.device = device
         self.k = [torch.zeros(CAP, HKV * D, dtype=torch.bfloat16, device=device) for _ in range(LAYERS)]
         self.v = [torch.zeros(CAP, HKV * D, dtype=torch.bfloat16, device=device) for _ in range(LAYERS)]
@@ -87,14 +95,23 @@ class _Decoder:
         p = self.layers[i]
         t = x.shape[0]
         qkv = _rms(x, p["norm"]) @ p["w_qkv"].T
-        qg = qkv[:, : H * 2 * D].reshape(t, H, 2 * D)
-        q, gate = qg[..., :D], qg[..., D:]
-        k = qkv[:, H * 2 * D : H * 2 * D + HKV * D].reshape(t, HKV, D)
-        v = qkv[:, H * 2 * D + HKV * D :].reshape(t, HKV, D)
-        q = _rope(_rms(q, p["q_norm"]), positions)
-        k = _rope(_rms(k, p["k_norm"]), positions)
-        self.k[i][positions] = k.reshape(t, -1).to(torch.bfloat16)  # write before read
-        self.v[i][positions] = v.reshape(t, -1).to(torch.bfloat16)
+        if decode and self.prep_decode is not None:
+            # q/k norm + RoPE + cache writes at the device position in one call
+            q, gate = self.prep_decode(qkv.reshape(-1), p, self.k[i], self.v[i], self.pos)
+            q, gate = q.reshape(1, H, D), gate.reshape(1, H, D)
+        else:
+            qg = qkv[:, : H * 2 * D].reshape(t, H, 2 * D)
+            q, gate = qg[..., :D], qg[..., D:]
+            k = qkv[:, H * 2 * D : H * 2 * D + HKV * D].reshape(t, HKV, D)
+            v = qkv[:, H * 2 * D + HKV * D :].reshape(t, HKV, D)
+            if self.tables is not None:
+                q = _rope_tab(_rms(q, p["q_norm"]), positions, *self.tables)
+                k = _rope_tab(_rms(k, p["k_norm"]), positions, *self.tables)
+            else:
+                q = _rope(_rms(q, p["q_norm"]), positions)
+                k = _rope(_rms(k, p["k_norm"]), positions)
+            self.k[i][positions] = k.reshape(t, -1).to(torch.bfloat16)  # write before read
+            self.v[i][positions] = v.reshape(t, -1).to(torch.bfloat16)
         kc = self.k[i].view(CAP, HKV, D)
         vc = self.v[i].view(CAP, HKV, D)
         if decode:
@@ -162,4 +179,34 @@ def test_greedy_64_tokens_identical(hip_backend):
     hip_ids, _ = _Decoder(params, hip_prefill, hip_decode, dev).generate(prompt)
     print(f"[greedy] min top-1 margin {min(margins):.4f}, distinct ids {len(set(ref_ids))}", flush=True)
     assert len(hip_ids) == NEW
+    assert hip_ids == ref_ids, f"first divergence at step {next(i for i, (a, b) in enumerate(zip(hip_ids, ref_ids)) if a != b)}"
+
+
+def test_greedy_64_tokens_identical_with_fused_decode_prep(hip_backend):
+    """As above, and the HIP path also runs each decode step's q/k RMSNorm,
+    RoPE and bf16 cache writes as one ``attn_prep`` launch (layers.py:58-73)
+    instead of the torch operators; both paths rotate with the same tables."""
+    from oracle import prep as orp
+
+    dev = torch.device("cuda")
+    params = _params(dev)
+    prompt = params[3]
+    cos, sin = (t.to(dev) for t in orp.rope_tables(CAP, D, 10000.0))
+
+    def hip_prefill(q, k, v, scale):
+        return hip_backend.attention_prefill(q.to(torch.bfloat16), k, v, scale, torch.float32)
+
+    def hip_decode(q, k, v, pos, scale):
+        return hip_backend.attention_fixed(q.float().contiguous(), k, v, pos, scale)
+
+    def hip_prep(qkv, p, kc, vc, pos):
+        return hip_backend.attn_prep(qkv.contiguous(), p["q_norm"], p["k_norm"], 1e-6, cos, sin, pos, D,
+                                     kc, vc, H, HKV, D)
+
+    print("[greedy+prep] reference path", flush=True)
+    ref_ids, margins = _Decoder(params, _ref_prefill, _ref_decode, dev, tables=(cos, sin)).generate(prompt)
+    print("[greedy+prep] HIP path", flush=True)
+    hip_ids, _ = _Decoder(params, hip_prefill, hip_decode, dev, tables=(cos, sin),
+                          prep_decode=hip_prep).generate(prompt)
+    print(f"[greedy+prep] min top-1 margin {min(margins):.4f}, distinct ids {len(set(ref_ids))}", flush=True)
     assert hip_ids == ref_ids, f"first divergence at step {next(i for i, (a, b) in enumerate(zip(hip_ids, ref_ids)) if a != b)}"
