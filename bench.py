@@ -348,6 +348,47 @@ def main() -> int:
         log(f"decode prep: fused {fused_ms * 1e3:.2f} us/layer, unfused {split_ms_p * 1e3:.2f} us/layer")
         del pcaches
         torch.cuda.empty_cache()
+        # Gated DeltaNet decode step (backends.py:79-92): one launch per layer vs the
+        # reference's torch formulation (backends.py:242-271) on the same GPU.
+        gdn = {}
+        for name, hk_, hv_, nl in (("0.8B", 16, 16, 18), ("35B-A3B", 16, 32, 30)):
+            dg = 128
+            gg = torch.Generator().manual_seed(hv_)
+            gq = torch.randn(hk_, dg, generator=gg).to(dev)
+            gk = torch.randn(hk_, dg, generator=gg).to(dev)
+            gv = torch.randn(hv_, dg, generator=gg).to(dev)
+            glog = (-torch.rand(hv_, generator=gg) * 0.5).to(dev)
+            gbeta = torch.randn(hv_, generator=gg).to(dev)
+            states = [(torch.randn(hv_, dg, dg, generator=gg) * 0.1).to(dev) for _ in range(nl)]
+            sc = dg ** -0.5
+            kmap = torch.arange(hv_, device=dev) % hk_
+
+            def gdn_hip():
+                for st_ in states:
+                    backend.gdn_decode(gq, gk, gv, glog, gbeta, st_, sc)
+
+            def gdn_torch():
+                for st_ in states:
+                    qn_ = gq * torch.rsqrt(gq.pow(2).sum(-1, keepdim=True) + 1e-6) * sc
+                    kn_ = gk * torch.rsqrt(gk.pow(2).sum(-1, keepdim=True) + 1e-6)
+                    dec = st_ * torch.exp(glog).view(hv_, 1, 1)
+                    rec = torch.einsum("hdv,hd->hv", dec, kn_[kmap])
+                    dl = (gv - rec) * torch.sigmoid(gbeta).unsqueeze(-1)
+                    st_.copy_(dec + kn_[kmap].unsqueeze(-1) * dl.unsqueeze(-2))
+                    torch.einsum("hdv,hd->hv", st_, qn_[kmap])
+
+            hip_ms = time_graph(torch, gdn_hip, esteps, ewarm) / nl
+            torch_ms = time_graph(torch, gdn_torch, max(20, esteps // 5), 5) / nl
+            gbytes = 2 * hv_ * dg * dg * 4 + 2 * hk_ * dg * 4 + 2 * hv_ * dg * 4 + 2 * hv_ * 4
+            gdn[name] = {"heads_k": hk_, "heads_v": hv_, "dim": dg, "layers_per_graph": nl,
+                         "us_per_layer": round(hip_ms * 1e3, 3), "GBps": round(gbytes / (hip_ms * 1e-3) / 1e9, 1),
+                         "frac_hbm_peak": round(gbytes / (hip_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "bytes_per_layer": gbytes, "torch_gpu_us_per_layer": round(torch_ms * 1e3, 3)}
+            log(f"gdn {name}: {hip_ms * 1e3:.2f} us/layer ({gbytes / (hip_ms * 1e-3) / 1e9:.0f} GB/s), "
+                f"torch on GPU {torch_ms * 1e3:.2f} us/layer")
+            del states
+        extra["gdn_decode"] = gdn
+        torch.cuda.empty_cache()
 
     # ------------------------------------------------------------ CPU baseline
     cpu_baseline = None

@@ -69,6 +69,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _c_i32, _c_i32, _c_i32, _vp, _vp, _c_f32, _vp, _vp, _vp, _c_i32, _c_i32, _vp, _c_i32,
          _vp, _vp, _c_i64, _c_i64, _c_i32, _vp],
     ),
+    "bt_gdn_decode": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_f32, _c_f32, _vp, _vp],
+    ),
 }
 
 _lock = threading.Lock()

@@ -22,7 +22,9 @@ and adds the operators the reference runs outside the protocol:
   reference Backend's q/k norm and partial RoPE operators (backends.py:44-62);
 * ``attn_prep(...)``: the whole decode-step preparation of an attention layer
   (q/k RMSNorm + RoPE, bf16 cache writes at the device position) in one launch
-  (layers.py:58-73, graph.py:41-53).
+  (layers.py:58-73, graph.py:41-53);
+* ``gdn_decode(q, k, v, g, beta, state, scale, eps)``: the Gated DeltaNet
+  one-token step with the f32 state updated in place (backends.py:79-92).
 
 Every launch goes through libbreezetoken_amd.so on torch's current stream with
 no host synchronisation, so the calls can be captured in a hipGraph
@@ -472,6 +474,40 @@ class HipBackend:
         check("bt_attn_prep", rc)
         gate = qkv[: heads * 2 * D].view(heads, 2 * D)[:, D:]
         return q, gate
+
+    # ------------------------------------------------------------ GDN decode
+    def gdn_decode(
+        self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+        beta: torch.Tensor, state: torch.Tensor, scale: float, eps: float = 1e-6,
+    ) -> torch.Tensor:
+        """One gated-delta-rule step; updates ``state`` in place and returns ``o``
+        (backends.py:79-92, 242-271).  q/k (Hk, D), v (Hv, D), g/beta (Hv,),
+        state (Hv, D, D) f32 contiguous; value head h reads key head h % Hk."""
+        if q.shape != k.shape or q.ndim != 2 or v.ndim != 2:
+            raise ValueError("q/k must be (key_heads, dim); v must be (value_heads, dim)")
+        heads_k, dim = q.shape
+        heads_v = v.shape[0]
+        if heads_v % heads_k:
+            raise ValueError("value_heads must be a multiple of key_heads")
+        if state.shape != (heads_v, dim, dim):
+            raise ValueError(f"state shape {tuple(state.shape)} != {(heads_v, dim, dim)}")
+        for n, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta), ("state", state)):
+            self._check_f32_dev(n, t)
+        if not state.is_contiguous():
+            raise RuntimeError("the GDN state must be contiguous (it is updated in place)")
+        if dim not in (64, 128):
+            raise RuntimeError(f"GDN decode serves dim 64 or 128, got {dim}")
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        g, beta = g.reshape(-1).contiguous(), beta.reshape(-1).contiguous()
+        if g.numel() != heads_v or beta.numel() != heads_v:
+            raise ValueError("g and beta need one value per value head")
+        out = torch.empty((heads_v, dim), dtype=torch.float32, device=self._dev)
+        rc = self._lib.bt_gdn_decode(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), state.data_ptr(),
+            heads_k, heads_v, dim, float(scale), float(eps), out.data_ptr(), _stream(self._dev),
+        )
+        check("bt_gdn_decode", rc)
+        return out
 
     def close(self) -> None:
         self._ws.clear()

@@ -95,6 +95,21 @@ struct RowPrepParams {
   int32_t cache_cap;
 };
 
+// Gated DeltaNet single-token decode step (gdn_decode.hip).
+struct GdnParams {
+  const float* q;      // (heads_k, D)
+  const float* k;      // (heads_k, D)
+  const float* v;      // (heads_v, D)
+  const float* g;      // (heads_v,) log decay
+  const float* beta;   // (heads_v,) logits of the write strength
+  float* state;        // (heads_v, D, D), updated in place
+  float* out;          // (heads_v, D)
+  int32_t heads_k;
+  int32_t heads_v;
+  float scale;
+  float eps;
+};
+
 // Keys per block of the prefill key loop, and the size of the transposed fp16
 // V image the prefill builds in its workspace: per kv head and 64-key block,
 // 8 chunks of 8 keys x head_dim rows x 16 bytes, for kv_len keys.
@@ -129,5 +144,6 @@ hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_row_norm_rope(const RowPrepParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_attn_prep(const RowPrepParams& p, int head_dim, hipStream_t stream);
+hipError_t launch_gdn_decode(const GdnParams& p, int dim, hipStream_t stream);
 
 }  // namespace bt

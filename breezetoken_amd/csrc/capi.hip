@@ -372,4 +372,27 @@ int bt_attn_prep(const float* qkv, int32_t heads, int32_t kv_heads, int32_t head
   return hip_rc(bt::launch_attn_prep(p, head_dim, (hipStream_t)stream));
 }
 
+int bt_gdn_decode(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                  float* state, int32_t heads_k, int32_t heads_v, int32_t dim, float scale, float eps,
+                  float* out, void* stream) {
+  if (!q || !k || !v || !g || !beta || !state || !out) return BT_EINVAL;
+  if (heads_k < 1 || heads_v < 1 || heads_v % heads_k || dim < 1) return BT_EINVAL;
+  if (!aligned16(v) || !aligned16(state) || !aligned16(out)) return BT_EINVAL;
+  if (!(eps >= 0.f)) return BT_EINVAL;
+  if (dim != 64 && dim != 128) return BT_ENOTSUP;
+  bt::GdnParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = g;
+  p.beta = beta;
+  p.state = state;
+  p.out = out;
+  p.heads_k = heads_k;
+  p.heads_v = heads_v;
+  p.scale = scale;
+  p.eps = eps;
+  return hip_rc(bt::launch_gdn_decode(p, dim, (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -180,6 +180,18 @@ int bt_attn_prep(const float* qkv, int32_t heads, int32_t kv_heads, int32_t head
                  void* q_out, int32_t q_dtype, void* cache_k, void* cache_v, int64_t kv_stride_tok,
                  int64_t kv_stride_head, int32_t cache_cap, void* stream);
 
+/* One-token Gated DeltaNet decode step with the f32 recurrent state updated
+ * in place.  Replaces Backend.gdn_decode (breezetoken/backends.py:79-92;
+ * torch form 242-271; kernel kernels/cuda/gdn.py:31-139) as called by
+ * LayerMixin._gdn (breezetoken/model/layers.py:104-108).  q, k (heads_k, dim),
+ * v (heads_v, dim), g and beta (heads_v,) f32; state (heads_v, dim, dim) f32
+ * contiguous, row index = key dim, column = value dim; out (heads_v, dim) f32.
+ * Value head h reads key head h % heads_k.  v, state and out 16-byte aligned;
+ * dim in {64, 128}; heads_v a multiple of heads_k. */
+int bt_gdn_decode(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                  float* state, int32_t heads_k, int32_t heads_v, int32_t dim, float scale, float eps,
+                  float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

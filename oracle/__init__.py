@@ -46,4 +46,10 @@ What each function restates, and what pins it (see ``tests/test_oracle.py``):
   (identity at 0, pair norms, composition), planted mistakes (sum for mean,
   missing weight or eps, flipped sign, interleaved pairs, wrong table row) and
   segment markers for the projection slicing.
+* ``gdn.torch_gdn_decode`` -- the Gated DeltaNet one-token step with the f32
+  state updated in place (breezetoken/backends.py:242-271).  Pinned by
+  (``tests/test_oracle_gdn.py``): a float64 loop written from the update rule,
+  closed forms (no write when beta -> -inf, zero state, the delta rule mapping
+  kn to v), the h % Hk head grouping, planted mistakes (g without exp, blocked
+  grouping, raw beta).
 """

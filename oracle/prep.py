@@ -98,3 +98,4 @@ def brute_rope_f64(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, pos: int, ro
             sign = -1.0 if d < half else 1.0
             out[r, d] = rows[r, d] * float(cos[pos, d]) + sign * rows[r, partner] * float(sin[pos, d])
     return out.reshape(x.shape)
+

@@ -191,3 +191,17 @@ def test_norm_rope_and_prep_refuse_bad_arguments_before_launching():
     assert lib.bt_attn_prep(*bad) == _lib.BT_EINVAL
     bad = list(args); bad[3] = 80; bad[10] = 64
     assert lib.bt_attn_prep(*bad) == _lib.BT_ENOTSUP
+
+
+def test_gdn_decode_refuses_bad_arguments_before_launching():
+    lib = _lib.lib()
+    fake = 1 << 20
+    ok = [fake, fake, fake, fake, fake, fake, 16, 16, 128, 0.088, 1e-6, fake, None]
+    bad = list(ok); bad[5] = None                  # null state
+    assert lib.bt_gdn_decode(*bad) == _lib.BT_EINVAL
+    bad = list(ok); bad[7] = 12                    # value heads not a multiple of key heads
+    assert lib.bt_gdn_decode(*bad) == _lib.BT_EINVAL
+    bad = list(ok); bad[5] = fake + 4              # misaligned state
+    assert lib.bt_gdn_decode(*bad) == _lib.BT_EINVAL
+    bad = list(ok); bad[8] = 96                    # unserved dim
+    assert lib.bt_gdn_decode(*bad) == _lib.BT_ENOTSUP
