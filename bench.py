@@ -389,6 +389,31 @@ def main() -> int:
             del states
         extra["gdn_decode"] = gdn
         torch.cuda.empty_cache()
+        # decode matvec (backends.py:36-37): the vocabulary head and the 0.8B projections, with
+        # enough distinct weight copies per graph to stream from HBM (> 256 MB MALL), against
+        # torch's bf16 matmul (vendor BLAS) on the same weights.
+        gemv = {}
+        for name, K, N in (("head", 1024, 248320), ("attn_qkv", 1024, 5120), ("mlp_gate_up", 1024, 7168),
+                           ("mlp_down", 3584, 1024)):
+            copies = max(1, -(-384 * 2**20 // (K * N * 2)))
+            gw = torch.Generator().manual_seed(K + N)
+            xs_ = torch.randn(K, generator=gw).to(dev)
+            wts = [torch.randn(K, N, generator=gw).to(torch.bfloat16).to(dev) for _ in range(copies)]
+            xb = xs_.to(torch.bfloat16).reshape(1, K)
+            hip_ms = time_graph(torch, lambda: [backend.linear(xs_, w_) for w_ in wts],
+                                max(20, esteps // 5), 5) / copies
+            blas_ms = time_graph(torch, lambda: [torch.matmul(xb, w_) for w_ in wts],
+                                 max(20, esteps // 5), 5) / copies
+            wbytes = K * N * 2 + K * 4 + N * 4
+            gemv[name] = {"K": K, "N": N, "copies_per_graph": copies, "us_per_call": round(hip_ms * 1e3, 3),
+                          "GBps": round(wbytes / (hip_ms * 1e-3) / 1e9, 1),
+                          "frac_hbm_peak": round(wbytes / (hip_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                          "torch_bf16_matmul_us": round(blas_ms * 1e3, 3)}
+            log(f"gemv {name} {K}x{N}: {hip_ms * 1e3:.2f} us ({wbytes / (hip_ms * 1e-3) / 1e9:.0f} GB/s), "
+                f"torch bf16 matmul {blas_ms * 1e3:.2f} us")
+            del wts
+            torch.cuda.empty_cache()
+        extra["gemv"] = gemv
 
     # ------------------------------------------------------------ CPU baseline
     cpu_baseline = None

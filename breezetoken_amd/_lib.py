@@ -73,6 +73,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_f32, _c_f32, _vp, _vp],
     ),
+    "bt_gemv_workspace_bytes": (_c_i64, [_c_i32, _c_i32]),
+    "bt_gemv_bf16": (
+        ctypes.c_int,
+        [_vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _c_i64, _vp],
+    ),
 }
 
 _lock = threading.Lock()

@@ -24,7 +24,9 @@ and adds the operators the reference runs outside the protocol:
   (q/k RMSNorm + RoPE, bf16 cache writes at the device position) in one launch
   (layers.py:58-73, graph.py:41-53);
 * ``gdn_decode(q, k, v, g, beta, state, scale, eps)``: the Gated DeltaNet
-  one-token step with the f32 state updated in place (backends.py:79-92).
+  one-token step with the f32 state updated in place (backends.py:79-92);
+* ``linear(x, w)``: the decode matvec x (K,) f32 . w (K, N) bf16 -> (N,) f32
+  of every projection and the vocabulary head (backends.py:36-37).
 
 Every launch goes through libbreezetoken_amd.so on torch's current stream with
 no host synchronisation, so the calls can be captured in a hipGraph
@@ -474,6 +476,35 @@ class HipBackend:
         check("bt_attn_prep", rc)
         gate = qkv[: heads * 2 * D].view(heads, 2 * D)[:, D:]
         return q, gate
+
+    # ---------------------------------------------------------- decode matvec
+    def linear(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """One decode matvec: ``x`` (..., K) f32 times ``w`` (K, N) bf16 -> (N,)
+        f32 (backends.py:36-37, 620-630; x.numel() == K as in _torch_linear,
+        182-184)."""
+        K, N = w.shape
+        if x.shape[-1] != K:
+            raise ValueError(f"linear shape mismatch: x {tuple(x.shape)}, w {tuple(w.shape)}")
+        if x.numel() != K:
+            raise ValueError("linear is a matvec: x must hold exactly K values")
+        self._check_f32_dev("x", x)
+        if w.dtype != torch.bfloat16 or w.device != self._dev or w.stride(1) != 1:
+            raise RuntimeError("w must be a bf16 (K, N) device tensor with unit column stride")
+        if N % 8 or w.stride(0) % 8 or w.data_ptr() % 16:
+            raise RuntimeError("w needs N and its row stride in multiples of 8 and 16-byte alignment")
+        x = x.reshape(-1).contiguous()
+        nbytes = int(self._lib.bt_gemv_workspace_bytes(K, N))
+        ws = None
+        if nbytes:
+            ws = self._ws.get(("gemv", K, N))
+            if ws is None:
+                ws = torch.empty(nbytes, dtype=torch.uint8, device=self._dev)
+                self._ws[("gemv", K, N)] = ws  # kept: captured graphs may point at it
+        y = torch.empty(N, dtype=torch.float32, device=self._dev)
+        rc = self._lib.bt_gemv_bf16(x.data_ptr(), w.data_ptr(), w.stride(0), K, N, y.data_ptr(), _ptr(ws),
+                                    nbytes, _stream(self._dev))
+        check("bt_gemv_bf16", rc)
+        return y
 
     # ------------------------------------------------------------ GDN decode
     def gdn_decode(

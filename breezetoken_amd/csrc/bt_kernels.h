@@ -110,6 +110,46 @@ struct GdnParams {
   float eps;
 };
 
+// Decode matvec y = x . W (gemv.hip).
+struct GemvParams {
+  const float* x;        // (K,) f32
+  const uint16_t* w;     // (K, N) bf16, row stride ldw elements
+  int64_t ldw;
+  int32_t K;
+  int32_t N;
+  int32_t splits;        // shares of K (SK); 1: no partials
+  float* partial;        // (SK, N) f32 when SK > 1
+  float* y;              // (N,) f32
+};
+
+// Launch shape of the matvec: VEC columns per lane (tile = 64*VEC columns)
+// and the number of K shares.  A wide matrix (>= 256 tiles of 512 columns,
+// e.g. the vocabulary head) is not split: every CU already streams whole
+// columns.  Otherwise K is split so that about 512 work-groups stream W with
+// at least 64 rows per share (measured on MI355X against 256/1024/2048/4096
+// groups and 16/32/128 rows).
+constexpr int kGemvTargetGroups = 512;
+constexpr int kGemvMinRows = 64;
+inline void gemv_shape(int K, int N, int* vec, int* splits, int* tiles) {
+  const int tiles8 = (N + 511) / 512;
+  *vec = tiles8 >= 8 ? 8 : 4;
+  *tiles = (N + 64 * *vec - 1) / (64 * *vec);
+  if (tiles8 >= 256) {
+    *splits = 1;
+    return;
+  }
+  const int sk = (kGemvTargetGroups + *tiles - 1) / *tiles;
+  const int cap = K / kGemvMinRows > 1 ? K / kGemvMinRows : 1;
+  *splits = sk < 1 ? 1 : (sk > cap ? cap : sk);
+}
+
+// Workspace of the split-K matvec: the partial rows.
+inline size_t gemv_workspace_bytes(int K, int N) {
+  int vec, sk, tiles;
+  gemv_shape(K, N, &vec, &sk, &tiles);
+  return sk == 1 ? 0 : (size_t)sk * N * 4;
+}
+
 // Keys per block of the prefill key loop, and the size of the transposed fp16
 // V image the prefill builds in its workspace: per kv head and 64-key block,
 // 8 chunks of 8 keys x head_dim rows x 16 bytes, for kv_len keys.
@@ -145,5 +185,6 @@ hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stre
 hipError_t launch_row_norm_rope(const RowPrepParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_attn_prep(const RowPrepParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_gdn_decode(const GdnParams& p, int dim, hipStream_t stream);
+hipError_t launch_gemv(const GemvParams& p, int vec, hipStream_t stream);
 
 }  // namespace bt

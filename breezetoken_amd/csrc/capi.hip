@@ -395,4 +395,30 @@ int bt_gdn_decode(const float* q, const float* k, const float* v, const float* g
   return hip_rc(bt::launch_gdn_decode(p, dim, (hipStream_t)stream));
 }
 
+int64_t bt_gemv_workspace_bytes(int32_t K, int32_t N) {
+  if (K < 1 || N < 1) return 0;
+  return (int64_t)bt::gemv_workspace_bytes(K, N);
+}
+
+int bt_gemv_bf16(const float* x, const void* w, int64_t ldw, int32_t K, int32_t N, float* y,
+                 void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!x || !w || !y || K < 1 || N < 1 || ldw < N) return BT_EINVAL;
+  if (N % 8 || ldw % 8 || !aligned16(w)) return BT_EINVAL;
+  if ((int64_t)K * ldw * 2 > (int64_t)INT32_MAX) return BT_ENOTSUP;
+  int vec, sk, tiles;
+  bt::gemv_shape(K, N, &vec, &sk, &tiles);
+  const int64_t need = (int64_t)bt::gemv_workspace_bytes(K, N);
+  if (sk > 1 && (!workspace || !aligned16(workspace) || workspace_bytes < need)) return BT_ENOSPC;
+  bt::GemvParams p{};
+  p.x = x;
+  p.w = static_cast<const uint16_t*>(w);
+  p.ldw = ldw;
+  p.K = K;
+  p.N = N;
+  p.splits = sk;
+  p.partial = static_cast<float*>(workspace);
+  p.y = y;
+  return hip_rc(bt::launch_gemv(p, vec, (hipStream_t)stream));
+}
+
 }  // extern "C"

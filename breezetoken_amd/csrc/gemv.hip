@@ -1,0 +1,147 @@
+// Decode matvec y = x . W for gfx950: x (K,) f32, W (K, N) bf16 row-major,
+// y (N,) f32.
+//
+// Semantics follow Backend.linear (breezetoken/backends.py:36-37; torch form
+// _torch_linear 182-184: x.float() @ w.float()) as served by the reference's
+// split-K bf16 GEMV (kernels/cuda/gemv.py:18-40, selected by _CudaGemv,
+// backends.py:303-333): partial sums over SK shares of K, then their sum.
+// One deliberate difference: x stays f32 (the reference kernel rounds it to
+// bf16 first), so the result is closer to the f32 definition.
+//
+// MI355X layout: a work-group of 4 waves owns a tile of 64*VEC columns (VEC
+// consecutive bf16 per lane: one 16- or 8-byte load per row) over one share of
+// K; wave w takes rows k0 + w, k0 + w + 4, ... and keeps kRowsAhead rows of
+// loads in flight, so every byte of W is streamed once with non-temporal
+// buffer loads (rows are contiguous segments of 64*VEC*2 bytes; the buffer
+// range check turns loads past the matrix into zeros).  x[k] is wave-uniform
+// and read through the scalar cache.  The four waves' accumulators are summed
+// through LDS.  With SK > 1 each share writes a partial row and a second,
+// small kernel adds the shares in order, so the result is deterministic.  (A
+// one-launch variant in which the last share to arrive adds the others needs
+// a device-scope release per work-group, which writes back the L2 each time:
+// measured 4x slower on the vocabulary head.)
+#include "bt_common.h"
+#include "bt_kernels.h"
+
+namespace bt {
+
+namespace {
+
+constexpr int kGemvWaves = 4;
+constexpr int kRowsAhead = 8;
+
+template <typename T>
+__device__ __forceinline__ T uniform_load_gemv(const T* p, int i) {
+  return ((const __attribute__((address_space(4))) T*)(p))[i];
+}
+
+template <int VEC>
+struct GemvLoad;
+template <>
+struct GemvLoad<8> {
+  typedef u32x4 type;
+  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2 /* nt */);
+  }
+};
+template <>
+struct GemvLoad<4> {
+  typedef u32x2 type;
+  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 2 /* nt */);
+  }
+};
+
+template <int VEC>
+__device__ __forceinline__ void fma_row(float (&acc)[VEC], const typename GemvLoad<VEC>::type& w, float x) {
+#pragma unroll
+  for (int i = 0; i < VEC / 2; ++i) {
+    const uint32_t pair = w[i];
+    acc[2 * i] = fmaf(x, bf16_bits_to_f32(pair & 0xffffu), acc[2 * i]);
+    acc[2 * i + 1] = fmaf(x, bf16_bits_to_f32(pair >> 16), acc[2 * i + 1]);
+  }
+}
+
+}  // namespace
+
+template <int VEC>
+__global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams p) {
+  constexpr int kTile = 64 * VEC;
+  __shared__ float red[kGemvWaves][kTile];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = blockIdx.x;
+  const int s = blockIdx.y;
+  const int k_per = (p.K + p.splits - 1) / p.splits;
+  const int k0 = s * k_per;
+  const int k1 = min(p.K, k0 + k_per);
+  const int n0 = tile * kTile + lane * VEC;
+
+  // K * ldw * 2 < 2^31 is checked on the host.
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.w), (short)0, (int)(p.K * p.ldw * 2), 0x00020000);
+  const uint32_t col_off = (uint32_t)n0 * 2;
+  float acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+
+  // Rows k0 + wave + 4*j; kRowsAhead loads in flight per pass.
+  int k = k0 + wave;
+  for (; k + kGemvWaves * (kRowsAhead - 1) < k1; k += kGemvWaves * kRowsAhead) {
+    typename GemvLoad<VEC>::type wv[kRowsAhead];
+#pragma unroll
+    for (int j = 0; j < kRowsAhead; ++j)
+      wv[j] = GemvLoad<VEC>::load(wrs, (uint32_t)((k + kGemvWaves * j) * p.ldw) * 2 + col_off);
+#pragma unroll
+    for (int j = 0; j < kRowsAhead; ++j) fma_row<VEC>(acc, wv[j], uniform_load_gemv(p.x, k + kGemvWaves * j));
+  }
+  for (; k < k1; k += kGemvWaves) {
+    const typename GemvLoad<VEC>::type wv = GemvLoad<VEC>::load(wrs, (uint32_t)(k * p.ldw) * 2 + col_off);
+    fma_row<VEC>(acc, wv, uniform_load_gemv(p.x, k));
+  }
+
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) red[wave][lane * VEC + i] = acc[i];
+  __syncthreads();
+  for (int c = threadIdx.x; c < kTile; c += 256) {
+    const float v = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
+    const int n = tile * kTile + c;
+    if (n < p.N) {
+      if (p.splits == 1) p.y[n] = v;
+      else p.partial[(int64_t)s * p.N + n] = v;
+    }
+  }
+}
+
+// y[n] = sum over shares s = 0 .. SK-1 of partial[s][n], in that order; eight
+// shares' loads are issued before their adds.
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvParams p) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= p.N) return;
+  const float* col = p.partial + n;
+  float v = 0.f;
+  int sh = 0;
+  for (; sh + 8 <= p.splits; sh += 8) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = col[(int64_t)(sh + j) * p.N];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v += t[j];
+  }
+  for (; sh < p.splits; ++sh) v += col[(int64_t)sh * p.N];
+  p.y[n] = v;
+}
+
+hipError_t launch_gemv(const GemvParams& p, int vec, hipStream_t stream) {
+  const int tile = 64 * vec;
+  const dim3 grid((p.N + tile - 1) / tile, p.splits);
+  if (vec == 8) hipLaunchKernelGGL(gemv_bf16_kernel<8>, grid, dim3(256), 0, stream, p);
+  else if (vec == 4) hipLaunchKernelGGL(gemv_bf16_kernel<4>, grid, dim3(256), 0, stream, p);
+  else return hipErrorInvalidValue;
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  hipLaunchKernelGGL(gemv_reduce_kernel, dim3((p.N + 255) / 256), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace bt

@@ -192,6 +192,24 @@ int bt_gdn_decode(const float* q, const float* k, const float* v, const float* g
                   float* state, int32_t heads_k, int32_t heads_v, int32_t dim, float scale, float eps,
                   float* out, void* stream);
 
+/* Bytes of split-K partial rows bt_gemv_bf16 needs for a (K, N) weight (0 when
+ * it does not split K); like the other workspace sizes it replaces the
+ * reference's per-shape partial buffer (backends.py:327). */
+int64_t bt_gemv_workspace_bytes(int32_t K, int32_t N);
+
+/* Decode matvec y (N,) f32 = x (K,) f32 . w (K, N) bf16, w row-major with row
+ * stride ldw elements.  Replaces Backend.linear (breezetoken/backends.py:36-37;
+ * torch form 182-184) as served by the split-K bf16 GEMV of
+ * kernels/cuda/gemv.py:18-40 (selected at backends.py:303-333 and 620-630) for
+ * every decode projection and the vocabulary head (graph.py:81).  x stays f32
+ * (the reference kernel rounds it to bf16).  N and ldw multiples of 8, w 16-byte
+ * aligned, K * ldw * 2 < 2^31; `workspace` (16-byte aligned) holds
+ * bt_gemv_workspace_bytes(K, N) bytes (may be NULL when that is 0).  When K is
+ * split, a second small kernel adds the shares in a fixed order, so the result
+ * is deterministic. */
+int bt_gemv_bf16(const float* x, const void* w, int64_t ldw, int32_t K, int32_t N, float* y,
+                 void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -205,3 +205,15 @@ def test_gdn_decode_refuses_bad_arguments_before_launching():
     assert lib.bt_gdn_decode(*bad) == _lib.BT_EINVAL
     bad = list(ok); bad[8] = 96                    # unserved dim
     assert lib.bt_gdn_decode(*bad) == _lib.BT_ENOTSUP
+
+
+def test_gemv_refuses_bad_arguments_and_sizes_its_workspace():
+    lib = _lib.lib()
+    fake = 1 << 20
+    assert lib.bt_gemv_workspace_bytes(0, 8) == 0
+    assert lib.bt_gemv_workspace_bytes(1024, 1024) > 0          # small N: K is split
+    assert lib.bt_gemv_bf16(None, fake, 1024, 1024, 1024, fake, fake, 1 << 30, None) == _lib.BT_EINVAL
+    assert lib.bt_gemv_bf16(fake, fake, 1024, 1024, 1020, fake, fake, 1 << 30, None) == _lib.BT_EINVAL
+    assert lib.bt_gemv_bf16(fake, fake + 8, 1024, 1024, 1024, fake, fake, 1 << 30, None) == _lib.BT_EINVAL
+    assert lib.bt_gemv_bf16(fake, fake, 1024, 1024, 1024, fake, None, 0, None) == _lib.BT_ENOSPC
+    assert lib.bt_gemv_bf16(fake, fake, 1 << 20, 4096, 1024, fake, fake, 1 << 30, None) == _lib.BT_ENOTSUP
