@@ -305,7 +305,7 @@ def main() -> int:
             extra["c4_prefill_roofline"] = {
                 "bound": "mfma", "achieved": round(big["TFLOPs"], 1), "peak": BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(big["frac_bf16_peak"], 4), "steps": big["steps"],
-                "kernels": "prefill_vt_kernel<256> + gqa_prefill_kernel<256>",
+                "kernels": "prefill_vt8_kernel<256> + gqa_prefill8_kernel<256>",
                 "algorithmic_flops": wl.prefill_flops(big["steps"], 8, 256)}
         log("c4: " + json.dumps(pre))
         # decode-step preparation (q/k RMSNorm + RoPE + bf16 cache writes, layers.py:58-73)

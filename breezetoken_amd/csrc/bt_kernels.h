@@ -182,6 +182,9 @@ hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int gri
 hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads, int batch,
                                  hipStream_t stream);
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stream);
+// Two-waves-per-SIMD prefill (gqa_prefill8.hip) for group sizes 1, 2, 4, 8.
+bool prefill8_serves(int group, int head_dim);
+hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_row_norm_rope(const RowPrepParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_attn_prep(const RowPrepParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_gdn_decode(const GdnParams& p, int dim, hipStream_t stream);

@@ -305,6 +305,10 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   p.out_stride_tok = out_stride_tok;
   p.out_stride_head = out_stride_head;
   p.vt = static_cast<uint16_t*>(workspace);
+  // Group sizes 1, 2, 4, 8 at D = 128 / 256 run two waves per SIMD; other
+  // shapes take the one-wave-per-SIMD kernel.  Each writes its own fp16 V^T
+  // image (laid out for its MFMA shape) into the same workspace size.
+  if (bt::prefill8_serves(p.group, head_dim)) return hip_rc(bt::launch_prefill8(p, head_dim, (hipStream_t)stream));
   return hip_rc(bt::launch_prefill(p, head_dim, (hipStream_t)stream));
 }
 

@@ -408,10 +408,16 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       wait_older();  // K_{kb+1}
       barrier();
     };
-    for (int kb = 1; kb < nkb; kb += 2) {
+    // Every pass ends with a buffer-0 step, so no path reaches the loop head
+    // with a copy into buffer 1 in flight (the compiler would otherwise wait
+    // for every copy before the first buffer-1 read); an odd last block runs
+    // after the loop.
+    int kb = 1;
+    for (; kb + 1 < nkb; kb += 2) {
       step(Buf<1>{}, kb);
-      if (kb + 1 < nkb) step(Buf<0>{}, kb + 1);
+      step(Buf<0>{}, kb + 1);
     }
+    if (kb < nkb) step(Buf<1>{}, kb);
     wait_all();  // V_last (and the last, unread K copy)
     barrier();
     // P of the last block, keys 32..63; V_last arrived in buffer last % 2

@@ -1,0 +1,402 @@
+// Causal GQA prefill on CDNA4 bf16/f16 MFMA with two waves per SIMD.
+//
+// Same contract as gqa_prefill.hip (the causal SDPA of prefill.py:56-68 and
+// the banded chunked prefill of qwen36_moe.py:394-428: query row i at
+// absolute position q_offset + i attends keys 0 .. q_offset + i), with a
+// work decomposition that keeps two waves resident on every SIMD:
+//  * a work-group of 8 waves shares one K tile and one V^T tile in LDS; wave w
+//    owns query head (w % G) of the kv group and 16 query positions
+//    [q0 + (w / G) * 16, +16), G in {1, 2, 4, 8};
+//  * per 64-key block a wave runs 32 v_mfma_f32_16x16x32_bf16 for S^T = K.Q^T
+//    (K from LDS, Q^T in registers) and 32 v_mfma_f32_16x16x32_f16 for
+//    O^T += V^T.P^T (V^T from LDS, P^T built in registers from the S^T
+//    accumulators).  Per wave that is 64 accumulators of O, 32 registers of Q
+//    and 16 of S -- half of the one-wave-per-SIMD layout -- so two waves fit
+//    in the register file and hide each other's LDS, copy and barrier waits;
+//  * the K tile lands in LDS row-major with an XOR swizzle: 16-byte chunk c of
+//    key row r sits in slot c ^ (r & 15) of the row.  Each copy instruction
+//    then reads whole contiguous rows from HBM/L2 (the swizzle is applied on
+//    the source side: lane l of a copy fetches the chunk that belongs in its
+//    slot), and the operand reads of 16 consecutive rows hit 16 different
+//    bank groups;
+//  * the V^T image (fp16) holds each 64-key block as 8 chunks of 8 keys; chunk
+//    c = kh*4 + g holds keys kh*32 + g*4 + {0,1,2,3} and kh*32 + 16 + g*4 +
+//    {0,1,2,3}: the order in which lane group g of the 16x16 result registers
+//    holds P for the 32-key half kh, so the P^T operand never moves between
+//    lanes;
+//  * the online softmax (log2 domain, lazy rescaling by 2^8) of block kb runs
+//    beside the P.V product of block kb - 1; tiles are double-buffered with
+//    two barriers per block and every copy issued as soon as its buffer is
+//    free, as in the one-wave kernel.
+#include "bt_common.h"
+#include "bt_kernels.h"
+
+namespace bt {
+
+namespace {
+
+typedef _Float16 halfx8_8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v_8 __attribute__((ext_vector_type(2)));
+typedef float float2v_8 __attribute__((ext_vector_type(2)));
+
+template <int B>
+struct Buf8 {
+  static constexpr int value = B;
+};
+
+constexpr int kKB8 = kPrefillKeyBlock;  // keys per block (64)
+constexpr int kWaves8 = 8;
+constexpr int kQ8 = 16;                 // query positions per wave
+constexpr float kLazy8 = 8.0f;          // log2-domain slack before the reference max moves
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc8(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 load16_8(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
+}
+// HBM -> LDS copy of 16 bytes per lane (lane l's bytes land at lds + 16 * l);
+// offsets past the descriptor's range read as zero.
+__device__ __forceinline__ void dma16_8(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff,
+                                        uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (BT_LDS void*)lds, 16, (int)voff, (int)soff, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma16_bf16(const u32x4& a, const u32x4& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma16_f16(const u32x4& a, const u32x4& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8_8, a), __builtin_bit_cast(halfx8_8, b), c,
+                                                0, 0, 0);
+}
+__device__ __forceinline__ uint32_t pack_rtz8(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+// Round to nearest even through a builtin (not asm), so the compiler sees the
+// VALU write and inserts the wait states an in-flight MFMA operand needs.
+__device__ __forceinline__ uint32_t pack_rne8(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2v_8){a, b}, half2v_8));
+}
+
+}  // namespace
+
+// Pre-pass: V (S, Hkv, D) bf16 -> fp16 V^T image for the 16x16 MFMA layout.
+// Key block b of kv head g is stored at vt + (g * nblk + b) * 64 * D; chunk c =
+// kh*4 + q (kh: 32-key half, q: lane group) holds at row d the 8 values
+// V[b*64 + key][d], key = kh*32 + q*4 + {0, 1, 2, 3, 16, 17, 18, 19} (16 bytes).
+// Keys past the prompt are zero.  Each thread transposes 8 x 8 tiles.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_vt8_kernel(PrefillParams p) {
+  constexpr int kDC = D / 8;
+  const int blk = blockIdx.x, g = blockIdx.y;
+  const int nblk = gridDim.x;
+  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+  const __amdgpu_buffer_rsrc_t vrs =
+      rsrc8(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)(p.q_offset + p.seqlen) * row_bytes);
+  uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kKB8 * D;
+  for (int item = threadIdx.x; item < 8 * kDC; item += 256) {
+    const int c = item / kDC, dc = item % kDC;
+    u32x4 rows[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = blk * kKB8 + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16;
+      rows[j] = load16_8(vrs, (uint32_t)key * row_bytes + (uint32_t)dc * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // output row d = dc*8 + i
+      u32x4 o;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t w0 = rows[2 * m][i >> 1], w1 = rows[2 * m + 1][i >> 1];
+        const float f0 = __uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16));
+        const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
+        o[m] = pack_rtz8(f0, f1);
+      }
+      *reinterpret_cast<u32x4*>(img + ((size_t)c * D + dc * 8 + i) * 8) = o;
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillParams p) {
+  constexpr int kDSteps = D / 32;      // K-dimension steps of Q.K^T (32 per MFMA)
+  constexpr int kDTiles = D / 16;      // 16-row d tiles of O^T
+  constexpr int kImg = kKB8 * D * 2;   // bytes of one K or V^T tile
+  constexpr int kCopies = kImg / 1024 / kWaves8;  // 1 KiB copies per wave per tile
+
+  // Separate LDS arrays so the compiler can see that copies into one buffer
+  // never alias operand reads from another; the key loop is unrolled by two so
+  // every buffer choice is a constant.
+  __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[kImg];
+  __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[kImg];
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kImg];
+  __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[kImg];
+  auto k_buf = [&](auto b) -> unsigned char* {
+    if constexpr (decltype(b)::value == 0) return k_lds0; else return k_lds1;
+  };
+  auto v_buf = [&](auto b) -> unsigned char* {
+    if constexpr (decltype(b)::value == 0) return v_lds0; else return v_lds1;
+  };
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int kvh = blockIdx.y;
+  const int G = p.group;                    // 1, 2, 4 or 8 (checked by the launcher)
+  const int pos_per_wg = kQ8 * (kWaves8 / G);
+  const int S = p.seqlen;
+  const int P0 = p.q_offset;
+  const int nkeys = P0 + S;
+  const int nqb = (S + pos_per_wg - 1) / pos_per_wg;
+  const int nblk = (nkeys + kKB8 - 1) / kKB8;
+  const int qblk = nqb - 1 - (int)blockIdx.x;  // heavy blocks first
+  const int wg_q0 = qblk * pos_per_wg;
+  const int q0 = wg_q0 + (wave / G) * kQ8;
+  const int wg_qend = min(S, wg_q0 + pos_per_wg);
+  const int nkb = (P0 + wg_qend + kKB8 - 1) / kKB8;
+  const int last = nkb - 1;
+  const int head = kvh * G + wave % G;
+
+  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+  const __amdgpu_buffer_rsrc_t krs = rsrc8(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)nkeys * row_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = rsrc8(p.vt + (size_t)kvh * nblk * kKB8 * D, (uint32_t)nblk * kImg);
+  constexpr int kSlots = D / 8;                // 16-byte chunks per key row
+  constexpr int kRowsPerCopy = 64 / kSlots;    // key rows per 1 KiB copy
+  static_assert(kSlots >= 16, "the row swizzle uses 16 slots");
+  const uint32_t v_voff = (uint32_t)lane * 16;
+  // K copy i (1 KiB) fills rows kRowsPerCopy*i .. of the tile: lane l fetches,
+  // for its slot s = l % kSlots of row r, the chunk s ^ (r & 15).  V^T copy i
+  // is bytes [1024 i, +1024) of the block's image.  Wave w issues copies w,
+  // w + 8, ...
+  uint32_t k_voff[kCopies];
+#pragma unroll
+  for (int j = 0; j < kCopies; ++j) {
+    const int r = (wave + kWaves8 * j) * kRowsPerCopy + lane / kSlots;
+    const int slot = lane % kSlots;
+    k_voff[j] = (uint32_t)r * row_bytes + (uint32_t)(slot ^ (r & 15)) * 16;
+  }
+  auto copy_k = [&](auto b, int kb) {
+    const uint32_t so = (uint32_t)(kb * kKB8) * row_bytes;
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j) {
+      const int i = wave + kWaves8 * j;
+      dma16_8(krs, k_buf(b) + i * 1024, k_voff[j], so);
+    }
+  };
+  auto copy_v = [&](auto b, int kb) {
+    const uint32_t so = (uint32_t)kb * kImg;
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j) {
+      const int i = wave + kWaves8 * j;
+      dma16_8(vrs, v_buf(b) + i * 1024, v_voff, so + (uint32_t)i * 1024);
+    }
+  };
+  // Each wave waits for its own copies; the barrier that follows publishes
+  // them.  wait_all: vmcnt(0); wait_older: all but the 2 * kCopies youngest.
+  auto wait_all = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };
+  constexpr int kYoung = 2 * kCopies;
+  constexpr int kWaitOlder = 0x0f70 | (kYoung & 0xf) | ((kYoung >> 4) << 14);
+  static_assert(kYoung < 64, "vmcnt holds 6 bits");
+  auto wait_older = [] { __builtin_amdgcn_s_waitcnt(kWaitOlder); };
+  // Work-group barrier without __syncthreads' fence (which would wait for
+  // every copy in flight); the LDS reads before it were consumed by MFMAs.
+  auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+  const int i16 = lane & 15;   // query column of the 16x16 tiles
+  const int g4 = lane >> 4;    // lane group: k slice of the operands, rows 4*g4.. of results
+  const float c_log2 = p.scale_log2;
+
+  // Q^T operand: lane holds Q[q0 + i16][st*32 + g4*8 .. +8] for each 32-d step.
+  u32x4 qop[kDSteps];
+  {
+    const int qrow = min(q0 + i16, S - 1);
+    const uint16_t* qp = p.q + (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + g4 * 8;
+#pragma unroll
+    for (int st = 0; st < kDSteps; ++st) qop[st] = *reinterpret_cast<const u32x4*>(qp + st * 32);
+  }
+
+  floatx4 oacc[kDTiles];
+#pragma unroll
+  for (int i = 0; i < kDTiles; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -INFINITY;          // reference max (log2 domain) of this lane's query column
+  float l_run = 0.f;                // partial row sum over this lane's keys
+  const int my_q = q0 + i16;
+  const int my_pos = P0 + my_q;     // keys 0 .. my_pos
+  u32x4 pk[2];                      // P of the pending block: 32-key halves, fp16
+
+  // S^T (64 keys x 16 queries) = K . Q^T from K buffer b: A operand of d-step
+  // st / key sub-tile sub is chunk st*4 + g4 of key row sub*16 + i16, stored
+  // in slot (st*4 + g4) ^ i16 of that row (row & 15 == i16).
+  auto qk = [&](auto b, floatx4 (&sacc)[4]) {
+    const unsigned char* kb_ = k_buf(b);
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < kDSteps; ++st) {
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(kb_ + (sub * 16 + i16) * (D * 2) +
+                                                          (((st * 4 + g4) ^ i16) * 16));
+        sacc[sub] = mfma16_bf16(a, qop[st], st == 0 ? zero : sacc[sub]);
+      }
+    }
+  };
+  // O^T += V^T . P^T over the 64 keys of V^T buffer b: A operand of key half kh
+  // / d tile dt is chunk kh*4 + g4 of row dt*16 + i16.
+  auto pv = [&](auto b, const u32x4 (&pp)[2]) {
+    const unsigned char* vb_ = v_buf(b);
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(vb_ + ((kh * 4 + g4) * D + dt * 16 + i16) * 16);
+        oacc[dt] = mfma16_f16(a, pp[kh], oacc[dt]);
+      }
+    }
+  };
+  // Causal mask of block kb: score of key sub*16 + g4*4 + r for query my_q.
+  auto mask = [&](int kb, floatx4 (&sacc)[4]) {
+    const int key0 = kb * kKB8 + g4 * 4;
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = key0 + sub * 16 + r;
+        sacc[sub][r] = key <= my_pos ? sacc[sub][r] : -INFINITY;
+      }
+  };
+  // Online softmax of one block: max over the 64 keys of the column (this
+  // lane's 16 and three lane groups' via xor 16 / 32), lazy reference update,
+  // P as fp16 in the MFMA key order; returns the factor O must be scaled by.
+  auto softmax = [&](floatx4 (&sacc)[4], u32x4 (&out)[2]) -> float {
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[sub][r]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = halves_max(tmax) * c_log2;
+    const bool move = tmax > m_ref + kLazy8;
+    const float m_new = move ? tmax : m_ref;
+    const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
+    m_ref = m_new;
+    const float neg_m = m_ref == -INFINITY ? 0.f : -m_ref;
+    float psum = 0.f;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const floatx4& s = sacc[2 * kh + (j >> 1)];
+        const float e0 = fast_exp2(fmaf(s[(j & 1) * 2], c_log2, neg_m));
+        const float e1 = fast_exp2(fmaf(s[(j & 1) * 2 + 1], c_log2, neg_m));
+        psum += e0 + e1;
+        out[kh][j] = pack_rne8(e0, e1);
+      }
+    }
+    l_run = l_run * alpha + psum;
+    return alpha;
+  };
+  auto rescale = [&](float alpha) {
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max moved by > 2^8
+#pragma unroll
+      for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
+    }
+  };
+  const int kb_diag = (P0 + q0 + 1) / kKB8;  // earlier blocks need no mask
+
+  // Copy schedule (as in the one-wave kernel):
+  //   start of step kb: V_kb -> V buffer kb % 2; after the mid barrier: K_{kb+2}
+  //   -> K buffer kb % 2; the mid barrier publishes V_{kb-1}, the end barrier
+  //   K_{kb+1}.  Copies past the last block re-read the last block.
+  copy_k(Buf8<0>{}, 0);
+  copy_k(Buf8<1>{}, min(1, last));
+  copy_v(Buf8<0>{}, 0);
+  wait_all();
+  __syncthreads();
+  {
+    floatx4 sacc[4];
+    qk(Buf8<0>{}, sacc);
+    barrier();
+    copy_k(Buf8<0>{}, min(2, last));
+    if (0 >= kb_diag) mask(0, sacc);
+    softmax(sacc, pk);  // O is still zero: its factor does not matter
+    barrier();
+  }
+  // Block kb: A: S_kb = K_kb . Q^T; B: O += V_{kb-1} . P_{kb-1} beside the
+  // softmax of S_kb.
+  auto step = [&](auto b, int kb) {
+    constexpr int B = decltype(b)::value;
+    copy_v(b, kb);
+    floatx4 sacc[4];
+    qk(b, sacc);
+    wait_older();  // V_{kb-1}
+    barrier();
+    copy_k(b, min(kb + 2, last));
+    if (kb >= kb_diag) mask(kb, sacc);
+    pv(Buf8<B ^ 1>{}, pk);
+    u32x4 pk_next[2];
+    const float alpha = softmax(sacc, pk_next);
+    rescale(alpha);
+    pk[0] = pk_next[0];
+    pk[1] = pk_next[1];
+    wait_older();  // K_{kb+1}
+    barrier();
+  };
+  // Every pass of the loop ends with a buffer-0 step, so no path reaches the
+  // loop head with a copy into buffer 1 in flight (the compiler would have to
+  // wait for every copy before the first buffer-1 read); an odd last block
+  // runs after the loop.
+  int kb = 1;
+  for (; kb + 1 < nkb; kb += 2) {
+    step(Buf8<1>{}, kb);
+    step(Buf8<0>{}, kb + 1);
+  }
+  if (kb < nkb) step(Buf8<1>{}, kb);
+  wait_all();
+  barrier();
+  if (last & 1) pv(Buf8<1>{}, pk); else pv(Buf8<0>{}, pk);
+
+  // ---- epilogue: row sums over the four lane groups, normalise, store -------
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run = halves_sum(l_run);
+  if (q0 < S && my_q < S) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    const int64_t orow = (int64_t)my_q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) {
+      const int d = dt * 16 + g4 * 4;
+      const float o0 = oacc[dt][0] * inv, o1 = oacc[dt][1] * inv, o2 = oacc[dt][2] * inv, o3 = oacc[dt][3] * inv;
+      if (p.out_bf16) {
+        const u32x2 pk2 = {pack2(f32_to_bf16_bits(o0), f32_to_bf16_bits(o1)),
+                           pack2(f32_to_bf16_bits(o2), f32_to_bf16_bits(o3))};
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
+      } else {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = float4{o0, o1, o2, o3};
+      }
+    }
+  }
+}
+
+bool prefill8_serves(int group, int head_dim) {
+  return (group == 1 || group == 2 || group == 4 || group == 8) && (head_dim == 128 || head_dim == 256);
+}
+
+hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t stream) {
+  const int pos_per_wg = kQ8 * (kWaves8 / p.group);
+  const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
+  const int nblk = (p.q_offset + p.seqlen + kKB8 - 1) / kKB8;
+  const dim3 grid(nqb, p.kv_heads), vt_grid(nblk, p.kv_heads);
+  switch (head_dim) {
+    case 128:
+      hipLaunchKernelGGL(prefill_vt8_kernel<128>, vt_grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(gqa_prefill8_kernel<128>, grid, dim3(kWaves8 * 64), 0, stream, p);
+      break;
+    case 256:
+      hipLaunchKernelGGL(prefill_vt8_kernel<256>, vt_grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(gqa_prefill8_kernel<256>, grid, dim3(kWaves8 * 64), 0, stream, p);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace bt
