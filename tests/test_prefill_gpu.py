@@ -78,8 +78,11 @@ def test_ragged_prompt_lengths(hip_backend, steps):
 
 
 @pytest.mark.parametrize("heads,kv,dim", [(8, 2, 128), (4, 4, 256), (8, 4, 256), (16, 2, 256), (8, 8, 128),
-                                          (6, 2, 256), (12, 2, 128)])
+                                          (16, 2, 128), (4, 2, 128),
+                                          (6, 2, 256), (12, 2, 128), (10, 2, 256), (3, 1, 128)])
 def test_other_group_sizes(hip_backend, heads, kv, dim):
+    """Group sizes 1, 2, 4, 8 at D = 128 / 256 run the two-waves-per-SIMD kernel;
+    3, 5, 6 take the one-wave-per-SIMD kernel."""
     q, k, v, scale = _inputs(300, heads, kv, dim, seed=heads * 100 + kv)
     ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
     _close(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale), ref)
