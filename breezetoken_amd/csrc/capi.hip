@@ -4,6 +4,9 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "../../include/breezetoken_amd.h"
 #include "bt_kernels.h"
 
@@ -192,29 +195,59 @@ int32_t bt_ragged_plan(const int32_t* lens, int32_t batch, int32_t target_groups
                        int32_t* total_splits) {
   if (!lens || !work || !split_base || !split_count || !total_splits) return BT_EINVAL;
   if (batch < 1 || target_groups < 1) return BT_EINVAL;
-  int64_t sum = 0;
+  int32_t max_len = 1;
   for (int32_t b = 0; b < batch; ++b) {
     if (lens[b] < 0) return BT_EINVAL;
-    sum += lens[b];
+    max_len = std::max(max_len, lens[b]);
   }
+  // Splits of sequence b under a cap of T tokens per split: ceil(len / T),
+  // at least 1, at most one per 32 tokens and kMaxSplitsPerSeq.
+  auto splits_of = [](int32_t len, int32_t cap) {
+    int64_t ns = ((int64_t)len + cap - 1) / cap;
+    ns = std::min<int64_t>(ns, (len + 31) / 32);
+    ns = std::min<int64_t>(ns, bt::kMaxSplitsPerSeq);
+    return (int32_t)std::max<int64_t>(ns, 1);
+  };
+  auto count_at = [&](int32_t cap) {
+    int64_t n = 0;
+    for (int32_t b = 0; b < batch; ++b) n += splits_of(lens[b], cap);
+    return n;
+  };
+  // The smallest cap whose split total fits target_groups (the count only
+  // falls as the cap grows): every work-group then streams at most that many
+  // tokens and the batch runs in one round of target_groups work-groups per kv
+  // head.  A batch with more sequences than target_groups gets one split each.
+  int32_t lo = 1, hi = max_len;
+  while (lo < hi) {
+    const int32_t mid = lo + (hi - lo) / 2;
+    if (count_at(mid) <= target_groups) hi = mid;
+    else lo = mid + 1;
+  }
+  const int32_t cap = lo;
   int32_t total = 0;
   for (int32_t b = 0; b < batch; ++b) {
-    const int32_t tiles = (lens[b] + 31) / 32;
-    int64_t ns = sum > 0 ? ((int64_t)target_groups * lens[b] + sum - 1) / sum : 1;
-    if (ns > tiles) ns = tiles;
-    if (ns > bt::kMaxSplitsPerSeq) ns = bt::kMaxSplitsPerSeq;
-    if (ns < 1) ns = 1;
-    split_base[b] = total;
-    split_count[b] = (int32_t)ns;
+    const int32_t ns = splits_of(lens[b], cap);
     if ((int64_t)total + ns > work_capacity) return BT_ENOSPC;
-    for (int32_t s = 0; s < ns; ++s) {
-      int32_t* w = work + 4 * (int64_t)(total + s);
+    split_base[b] = total;
+    split_count[b] = ns;
+    total += ns;
+  }
+  // Work entries, longest splits first (when the grid takes more than one
+  // round, the long ones start early).
+  std::vector<int32_t> order(batch);
+  for (int32_t b = 0; b < batch; ++b) order[b] = b;
+  std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t c) {
+    return (int64_t)lens[a] * split_count[c] > (int64_t)lens[c] * split_count[a];
+  });
+  int64_t i = 0;
+  for (const int32_t b : order) {
+    for (int32_t s = 0; s < split_count[b]; ++s, ++i) {
+      int32_t* w = work + 4 * i;
       w[0] = b;
       w[1] = s;
-      w[2] = (int32_t)ns;
-      w[3] = total;
+      w[2] = split_count[b];
+      w[3] = split_base[b];
     }
-    total += (int32_t)ns;
   }
   *total_splits = total;
   return total;

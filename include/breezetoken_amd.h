@@ -98,10 +98,13 @@ int bt_gqa_decode(const void* q, int32_t q_dtype, int64_t q_stride_seq, const vo
                   int64_t out_stride_seq, void* stream);
 
 /* Host-side planner for ragged batches (no device access): given host lengths
- * lens[batch], choose per-sequence split counts proportional to length so that
- * about `target_groups` work-groups per kv head exist, and fill
- *   work[4*i .. 4*i+3] = {b, s, ns_b, base_b} for every split i (capacity
- *   work_capacity entries), split_base[b], split_count[b], *total_splits.
+ * lens[batch], choose per-sequence split counts ns_b = ceil(len_b / T) (at
+ * least 1, at most ceil(len_b / 32)) for the smallest token cap T whose total
+ * fits `target_groups` work-groups per kv head (one split each when the batch
+ * is larger), and fill
+ *   work[4*i .. 4*i+3] = {b, s, ns_b, base_b}, one entry per split (capacity
+ *   work_capacity entries), longest splits first; split_base[b],
+ *   split_count[b], *total_splits.
  * Returns the number of work entries, or a negative BT_E* code. */
 int32_t bt_ragged_plan(const int32_t* lens, int32_t batch, int32_t target_groups,
                        int32_t* work, int32_t work_capacity, int32_t* split_base,

@@ -84,17 +84,44 @@ def _plan(lens, target):
     return n, list(work)[: 4 * max(n, 0)], list(base), list(cnt), tot.value
 
 
+def _tokens_per_split(L, ns):
+    return -(-L // ns)
+
+
 def test_ragged_plan_is_proportional_and_consistent():
     lens = [2591, 8912, 338, 24869, 0, 31, 32768]
     n, work, base, cnt, tot = _plan(lens, 128)
-    assert n == tot == sum(cnt)
+    assert n == tot == sum(cnt) <= 128
     for b, L in enumerate(lens):
         assert 1 <= cnt[b] <= max(1, -(-L // 32))
         assert base[b] == sum(cnt[:b])
     assert cnt[6] > cnt[3] > cnt[1] > cnt[0] > cnt[2]
     entries = [tuple(work[4 * i : 4 * i + 4]) for i in range(n)]
-    for i, (b, s, ns, bs) in enumerate(entries):
-        assert ns == cnt[b] and bs == base[b] and bs + s == i
+    # every split index base_b + s appears exactly once, with its sequence's count and base
+    assert sorted(bs + s for b, s, ns, bs in entries) == list(range(n))
+    for b, s, ns, bs in entries:
+        assert ns == cnt[b] and bs == base[b] and 0 <= s < ns
+    # longest splits first
+    sizes = [_tokens_per_split(lens[b], cnt[b]) for b, *_ in entries]
+    assert all(x >= y for x, y in zip(sizes, sizes[1:]))
+
+
+def test_ragged_plan_cap_is_the_smallest_that_fits():
+    """ns_b = ceil(len_b / T) for the smallest T with sum_b ns_b <= target: one round of
+    work-groups, and no smaller per-split token cap would fit (config-5 lengths)."""
+    from breezetoken_amd import workloads as wl
+
+    lens = wl.ragged_lengths()
+    for target in (128, 256, 40):
+        n, work, base, cnt, tot = _plan(lens, target)
+        assert tot <= target
+        cap = max(_tokens_per_split(L, c) for L, c in zip(lens, cnt))
+        assert all(c == max(1, min(-(-L // cap), -(-L // 32))) for L, c in zip(lens, cnt))
+        smaller = sum(max(1, min(-(-L // (cap - 1)), -(-L // 32))) for L in lens)
+        assert smaller > target
+    # more sequences than work-groups: one split each
+    n, work, base, cnt, tot = _plan(lens, 8)
+    assert cnt == [1] * len(lens) and tot == len(lens)
 
 
 def test_ragged_plan_rejects_bad_input():
