@@ -94,7 +94,8 @@ enum DecodeMode : int {
 // GMAX: 4 (groups of <= 4 query heads) or 8; D: head dim; WAVES: waves per
 // work-group; TILE: tokens a wave processes per step (16 or 32); PIPE: 1 =
 // one register buffer whose next tile is fetched as soon as it is consumed,
-// 2 = two register buffers (next tile in flight during the current one);
+// P > 1 = P register buffers, all filled at entry and each refilled right
+// after its tile is used (P tiles in flight);
 // MODE: a DecodeMode; QBF16: q is bf16 (else f32).
 template <int GMAX, int D, int WAVES, int TILE, int PIPE, int MODE, bool QBF16>
 __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeSplitParams p) {
@@ -268,9 +269,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
       load_k(tfirst, kr[0]);
       load_v(tfirst, vr[0]);
     }
-    if (PIPE == 2 && my_tiles > 1) {
-      load_k(tfirst + tstride, kr[PIPE - 1]);
-      load_v(tfirst + tstride, vr[PIPE - 1]);
+#pragma unroll
+    for (int b = 1; b < PIPE; ++b) {
+      if (b < my_tiles) {
+        load_k(tfirst + b * tstride, kr[b]);
+        load_v(tfirst + b * tstride, vr[b]);
+      }
     }
   }
 
@@ -424,18 +428,19 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
     for (int it = 0; it < my_tiles; ++it)
       compute(tfirst + it * tstride, it + 1 < my_tiles, kr[0], vr[0]);
   } else {
-    for (int it = 0; it < my_tiles; it += 2) {
-      const int ta = tfirst + it * tstride;
-      compute(ta, false, kr[0], vr[0]);
-      if (it + 2 < my_tiles) {
-        load_k(ta + 2 * tstride, kr[0]);
-        load_v(ta + 2 * tstride, vr[0]);
-      }
-      if (it + 1 >= my_tiles) break;
-      compute(ta + tstride, false, kr[PIPE - 1], vr[PIPE - 1]);
-      if (it + 3 < my_tiles) {
-        load_k(ta + 3 * tstride, kr[PIPE - 1]);
-        load_v(ta + 3 * tstride, vr[PIPE - 1]);
+    // Buffer b holds local tiles b, b + PIPE, ...; unrolled so every buffer
+    // index is a constant.
+    for (int it = 0; it < my_tiles; it += PIPE) {
+#pragma unroll
+      for (int b = 0; b < PIPE; ++b) {
+        if (it + b < my_tiles) {
+          const int t = tfirst + (it + b) * tstride;
+          compute(t, false, kr[b], vr[b]);
+          if (it + b + PIPE < my_tiles) {
+            load_k(t + PIPE * tstride, kr[b]);
+            load_v(t + PIPE * tstride, vr[b]);
+          }
+        }
       }
     }
   }
