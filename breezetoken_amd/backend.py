@@ -256,7 +256,9 @@ class HipBackend:
 
     # ----------------------------------------------------------- ragged decode
     def ragged_plan(self, lens: list[int], kv_heads: int, target_groups: int | None = None):
-        """Per-sequence split counts proportional to length, as device tables (cached)."""
+        """Split plan for a ragged batch, as device tables (cached): sequence b gets
+        ceil(len_b / T) splits for the smallest token cap T whose total fits
+        ``target_groups`` work-groups per kv head (default: one round, CUs / kv heads)."""
         if target_groups is None:
             target_groups = max(1, self.num_cus // max(1, kv_heads))
         key = (tuple(int(x) for x in lens), int(target_groups))
