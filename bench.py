@@ -134,6 +134,38 @@ def prefill_mode(torch, backend, dev, calls: int) -> int:
     return 0
 
 
+def ragged_mode(torch, backend, dev, calls: int) -> int:
+    """Config-5 ragged decode only (for rocprofv3 kernel traces): ``calls`` calls
+    over three copies of the cache after two warm-up calls, timed with HIP events
+    on the current stream."""
+    from breezetoken_amd import workloads as wl
+
+    rc5 = wl.c5_inputs()
+    rq = rc5.q.float().to(dev)
+    rkv = [(rc5.k.to(dev), rc5.v.to(dev)) for _ in range(3)]  # ~1 GB: the calls do not hit the MALL
+    roff = torch.tensor(rc5.offsets, dtype=torch.int64, device=dev)
+    rlen = torch.tensor(rc5.lens, dtype=torch.int32, device=dev)
+
+    def call(i):
+        rk, rv = rkv[i % len(rkv)]
+        backend.attention_ragged(rq, rk, rv, roff, rlen, rc5.lens, rc5.scale)
+
+    for i in range(2):
+        call(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(torch.cuda.current_stream())
+    for i in range(calls):
+        call(i)
+    end.record(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / calls
+    nbytes = 2 * sum(rc5.lens) * rc5.k.shape[1] * rc5.k.shape[2] * 2 + len(rc5.lens) * rq.shape[1] * rq.shape[2] * 4 * 2
+    print(json.dumps({"mode": "ragged", "sequences": len(rc5.lens), "tokens": sum(rc5.lens), "calls": calls,
+                      "us_per_call": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,10 +174,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--mode", choices=["bench", "pmc", "prefill"], default="bench",
+    ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "ragged"], default="bench",
                     help="pmc: only a 256 MiB device copy and the config-2 split kernel, "
                          "5 launches each, for rocprofv3 --pmc runs; prefill: only config-4 "
-                         "prefill at S=8192 (--steps calls), for kernel traces")
+                         "prefill at S=8192 (--steps calls), for kernel traces; ragged: only "
+                         "config-5 ragged decode (--steps calls), for kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
         print("this build measures one GPU only: the decode/prefill kernels run on a single "
@@ -171,6 +204,8 @@ def main() -> int:
         return pmc_mode(torch, backend, dev)
     if args.mode == "prefill":
         return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)))
+    if args.mode == "ragged":
+        return ragged_mode(torch, backend, dev, max(1, min(args.steps, 500)))
 
     def fixed_case(case, cap):
         cache = KVCache(cap, case.k.shape[1], case.k.shape[2], dev)
