@@ -141,6 +141,20 @@ def test_chunked_prefill_query_offset(hip_backend, steps, pos0):
     _close(out, ref)
 
 
+@pytest.mark.parametrize("heads,kv,dim,steps,pos0", [(8, 2, 256, 100, 37), (4, 4, 256, 70, 129), (8, 4, 128, 200, 64),
+                                                     (6, 2, 256, 90, 300)])
+def test_chunked_prefill_other_group_sizes(hip_backend, heads, kv, dim, steps, pos0):
+    """Query offsets for group sizes 4, 1, 2 (two-waves-per-SIMD kernel) and 3 (one-wave kernel)."""
+    g = torch.Generator().manual_seed(heads * 1000 + kv * 100 + pos0)
+    q = torch.randn(steps, heads, dim, generator=g).to(torch.bfloat16)
+    k = torch.randn(pos0 + steps, kv, dim, generator=g).to(torch.bfloat16)
+    v = torch.randn(pos0 + steps, kv, dim, generator=g).to(torch.bfloat16)
+    scale = dim**-0.5
+    print(f"[chunk] H={heads} Hkv={kv} D={dim} S={steps} pos0={pos0}", flush=True)
+    ref = orc.torch_prefill_banded(q.float(), k.float(), v.float(), pos0, scale)
+    _close(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, q_offset=pos0), ref)
+
+
 def test_chunked_prefill_head_major_cache(hip_backend):
     """The SDPA call of qwen36_moe.py:415-423 on views of a head-major
     (Hkv, capacity, D) cache, and the chunks together equal one full prefill."""
