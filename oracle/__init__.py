@@ -52,8 +52,10 @@ What each function restates, and what pins it (see ``tests/test_oracle.py``):
   closed forms (no write when beta -> -inf, zero state, the delta rule mapping
   kn to v), the h % Hk head grouping, planted mistakes (g without exp, blocked
   grouping, raw beta).
-* ``linear.torch_linear`` -- the decode matvec x.float() @ w.float()
-  (breezetoken/backends.py:182-184).  Pinned by (``tests/test_oracle_linear.py``):
+* ``linear.torch_linear`` / ``linear.split_k_linear`` -- the decode matvec
+  x.float() @ w.float() (breezetoken/backends.py:182-184), and the same product
+  as per-share partial sums added in order (kernels/cuda/gemv.py:18-40 with
+  backends.py:327-331), in float64.  Pinned by (``tests/test_oracle_linear.py``):
   float64 products with any number of K shares (split-K invariance), one-hot
   x selecting a row of w, linearity in x, and planted mistakes (transposed w,
   a dropped share).
