@@ -47,6 +47,8 @@ __device__ __forceinline__ int swz(int row, int slots) { return ((row & 7) * 2) 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+constexpr float kDecodeLazy = 8.0f;  // log2-domain slack before the reference max moves
+
 // K/V are streamed once per call: the non-temporal policy (nt) keeps them from
 // displacing reusable lines and measurably raises the stream rate on gfx950.
 constexpr int kPolicyStream = 2;  // gfx940+ cache-policy bits: nt
@@ -358,11 +360,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
     for (int i = 1; i < kVals; ++i) tmax = fmaxf(tmax, x[i]);
     tmax = wave_max_xor(tmax, 16);
     tmax = wave_max_xor(tmax, 32);
-    const float m_new = fmaxf(m_run, tmax);
-    // While every score so far is masked, m_new is -inf; subtract 0 instead so
-    // exp2 sees -inf (not NaN): p = 0 and alpha = 0 act on an O and l that are 0.
+    // Lazy reference max: m_run moves only when a score exceeds it by more
+    // than 2^8 (log2 domain), so p <= 2^8 and O / l are rescaled only then --
+    // behind a wave-uniform branch, almost never after the first tile.  The
+    // LSE stays exact: lse = log2(l) + m_run for whatever reference m_run is.
+    // While every score so far is masked, m_run is -inf and does not move
+    // (-inf > -inf + 8 is false); subtracting 0 then makes exp2 see -inf
+    // (not NaN), so p = 0 acts on an O and l that are 0.
+    const bool move = tmax > m_run + kDecodeLazy;
+    const float m_new = move ? tmax : m_run;
+    const float alpha = move ? fast_exp2(m_run - m_new) : 1.f;  // 0 when m_run is -inf
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
     float pr[kVals];
 #pragma unroll
     for (int i = 0; i < kVals; ++i) pr[i] = fast_exp2(x[i] - m_use);
@@ -371,8 +379,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
 #pragma unroll
     for (int i = 0; i < kVals; ++i) psum += pr[i];
     l_run = l_run * alpha + psum;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-    for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
+      for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
+    }
 
     // P^T operand: this lane's own probabilities, as bf16 hi or lo.
     uint32_t p16[kVals];
