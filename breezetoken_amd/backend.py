@@ -111,8 +111,10 @@ class HipBackend:
             self._ws[key] = ws  # kept until close(): captured graphs may point at it
         return ws
 
-    def _prefill_workspace(self, seqlen: int, kv_heads: int, dim: int) -> torch.Tensor:
-        nbytes = int(self._lib.bt_prefill_workspace_bytes(seqlen, kv_heads, dim))
+    def _prefill_workspace(self, steps: int, q_offset: int, heads: int, kv_heads: int, dim: int) -> torch.Tensor:
+        """Room for the V^T image and, where the library splits the key range
+        (short prompts, long cached prefixes), its partials."""
+        nbytes = int(self._lib.bt_prefill_split_workspace_bytes(steps, q_offset, heads, kv_heads, dim))
         ws = self._ws.get("prefill")
         if ws is None or ws.numel() < nbytes:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=self._dev)
@@ -341,7 +343,7 @@ class HipBackend:
         if k.stride() != v.stride():
             raise RuntimeError("k and v need identical strides")
         out = torch.empty((steps, heads, dim), dtype=out_dtype, device=self._dev)
-        ws = self._prefill_workspace(q_offset + steps, groups, dim)
+        ws = self._prefill_workspace(steps, q_offset, heads, groups, dim)
         rc = self._lib.bt_gqa_prefill(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1),
             k.stride(0), k.stride(1), steps, q_offset, heads, groups, dim, float(scale),

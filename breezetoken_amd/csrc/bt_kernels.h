@@ -66,7 +66,27 @@ struct PrefillParams {
   int out_bf16;
   int64_t out_stride_tok, out_stride_head;
   uint16_t* vt;        // workspace: fp16 V^T image, prefill_vt_bytes() bytes
+  // Split-key mode of the two-waves-per-SIMD kernel (kb_chunk > 0): work-group
+  // (query block, kv head, chunk c) covers key blocks [c*kb_chunk, +kb_chunk);
+  // a query block with more than one chunk writes one normalised partial and
+  // its log2-domain LSE per (query, head) row and chunk, merged by
+  // prefill_combine_kernel.  kb_chunk = 0: one work-group per query block.
+  int32_t kb_chunk;
+  int32_t max_chunks;  // chunks of the longest query block (grid z)
+  float* part;         // (kv_heads, query blocks, max_chunks, 128 rows, D) f32
+  float* lse;          // (kv_heads, query blocks, max_chunks, 128 rows) f32
 };
+
+// Split-key plan of the two-waves-per-SIMD prefill: used when one work-group
+// per query block would leave CUs idle (short prompts, long cached prefixes).
+struct PrefillSplitPlan {
+  int32_t kb_chunk = 0;    // 0: no split
+  int32_t max_chunks = 1;
+  int32_t query_blocks = 0;
+  size_t part_bytes = 0;   // partials + LSEs
+};
+PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv_heads, int head_dim,
+                                     int num_cus);
 
 // Per-row RMSNorm + RoPE (row mode) and the fused decode-step preparation
 // (attention mode); see attn_prep.hip.

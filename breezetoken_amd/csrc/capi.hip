@@ -291,6 +291,42 @@ int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t hea
   return (int64_t)bt::prefill_vt_bytes(kv_len, kv_heads, head_dim);
 }
 
+namespace {
+
+// Compute units of the current device, cached per device.
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  static int cache[64] = {0};
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
+}
+
+// The split-key plan bt_gqa_prefill uses for this shape on the current device
+// (kb_chunk 0: none), and where its partials start in the workspace.
+bt::PrefillSplitPlan prefill_plan(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
+                                  int32_t head_dim, int64_t* part_offset) {
+  *part_offset = align256((int64_t)bt::prefill_vt_bytes(q_offset + seqlen, kv_heads, head_dim));
+  const int group = heads / kv_heads;
+  if (!bt::prefill8_serves(group, head_dim)) return bt::PrefillSplitPlan{};
+  return bt::prefill8_split_plan(seqlen, q_offset, group, kv_heads, head_dim, device_cus());
+}
+
+}  // namespace
+
+int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
+                                         int32_t head_dim) {
+  if (seqlen < 1 || q_offset < 0 || heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 1) return 0;
+  if ((int64_t)q_offset + seqlen > INT32_MAX) return 0;
+  const int64_t vt = (int64_t)bt::prefill_vt_bytes(q_offset + seqlen, kv_heads, head_dim);
+  int64_t part_offset = 0;
+  const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
+  return plan.kb_chunk > 0 ? part_offset + (int64_t)plan.part_bytes : vt;
+}
+
 int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
                    int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
                    int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
@@ -340,8 +376,21 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   p.vt = static_cast<uint16_t*>(workspace);
   // Group sizes 1, 2, 4, 8 at D = 128 / 256 run two waves per SIMD; other
   // shapes take the one-wave-per-SIMD kernel.  Each writes its own fp16 V^T
-  // image (laid out for its MFMA shape) into the same workspace size.
-  if (bt::prefill8_serves(p.group, head_dim)) return hip_rc(bt::launch_prefill8(p, head_dim, (hipStream_t)stream));
+  // image (laid out for its MFMA shape) into the same workspace size.  When
+  // one work-group per query block would leave CUs idle and the workspace
+  // also holds bt_prefill_split_workspace_bytes, the key range is split.
+  if (bt::prefill8_serves(p.group, head_dim)) {
+    int64_t part_offset = 0;
+    const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
+    if (plan.kb_chunk > 0 && workspace_bytes >= part_offset + (int64_t)plan.part_bytes) {
+      p.kb_chunk = plan.kb_chunk;
+      p.max_chunks = plan.max_chunks;
+      p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_offset);
+      const size_t rows = (size_t)kv_heads * plan.query_blocks * plan.max_chunks * 128;
+      p.lse = p.part + rows * (size_t)head_dim;
+    }
+    return hip_rc(bt::launch_prefill8(p, head_dim, (hipStream_t)stream));
+  }
   return hip_rc(bt::launch_prefill(p, head_dim, (hipStream_t)stream));
 }
 

@@ -46,6 +46,8 @@ struct Buf8 {
 
 constexpr int kKB8 = kPrefillKeyBlock;  // keys per block (64)
 constexpr int kWaves8 = 8;
+constexpr int kRows8 = 128;             // (query, head) rows of a work-group: 8 waves x 16 queries
+constexpr int kMaxChunks = 64;          // split-key chunks per query block (combine LDS bound)
 constexpr int kQ8 = 16;                 // query positions per wave
 constexpr float kLazy8 = 8.0f;          // log2-domain slack before the reference max moves
 
@@ -154,7 +156,16 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   const int q0 = wg_q0 + (wave / G) * kQ8;
   const int wg_qend = min(S, wg_q0 + pos_per_wg);
   const int nkb = (P0 + wg_qend + kKB8 - 1) / kKB8;
-  const int last = nkb - 1;
+  // Key blocks [kb0, kb1) of this work-group: all of them, or chunk blockIdx.z.
+  const int chunk = blockIdx.z;
+  int kb0 = 0, kb1 = nkb, nchunks = 1;
+  if (p.kb_chunk > 0) {
+    kb0 = chunk * p.kb_chunk;
+    kb1 = min(nkb, kb0 + p.kb_chunk);
+    nchunks = (nkb + p.kb_chunk - 1) / p.kb_chunk;
+    if (kb0 >= kb1) return;  // this query block has fewer chunks (whole work-group)
+  }
+  const int last = kb1 - 1;
   const int head = kvh * G + wave % G;
 
   const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
@@ -307,17 +318,18 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   //   start of step kb: V_kb -> V buffer kb % 2; after the mid barrier: K_{kb+2}
   //   -> K buffer kb % 2; the mid barrier publishes V_{kb-1}, the end barrier
   //   K_{kb+1}.  Copies past the last block re-read the last block.
-  copy_k(Buf8<0>{}, 0);
-  copy_k(Buf8<1>{}, min(1, last));
-  copy_v(Buf8<0>{}, 0);
+  // Buffers alternate from the work-group's first block kb0.
+  copy_k(Buf8<0>{}, kb0);
+  copy_k(Buf8<1>{}, min(kb0 + 1, last));
+  copy_v(Buf8<0>{}, kb0);
   wait_all();
   __syncthreads();
   {
     floatx4 sacc[4];
     qk(Buf8<0>{}, sacc);
     barrier();
-    copy_k(Buf8<0>{}, min(2, last));
-    if (0 >= kb_diag) mask(0, sacc);
+    copy_k(Buf8<0>{}, min(kb0 + 2, last));
+    if (kb0 >= kb_diag) mask(kb0, sacc);
     softmax(sacc, pk);  // O is still zero: its factor does not matter
     barrier();
   }
@@ -345,19 +357,35 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   // loop head with a copy into buffer 1 in flight (the compiler would have to
   // wait for every copy before the first buffer-1 read); an odd last block
   // runs after the loop.
-  int kb = 1;
-  for (; kb + 1 < nkb; kb += 2) {
+  int kb = kb0 + 1;
+  for (; kb + 1 < kb1; kb += 2) {
     step(Buf8<1>{}, kb);
     step(Buf8<0>{}, kb + 1);
   }
-  if (kb < nkb) step(Buf8<1>{}, kb);
+  if (kb < kb1) step(Buf8<1>{}, kb);
   wait_all();
   barrier();
-  if (last & 1) pv(Buf8<1>{}, pk); else pv(Buf8<0>{}, pk);
+  if ((last - kb0) & 1) pv(Buf8<1>{}, pk); else pv(Buf8<0>{}, pk);
 
   // ---- epilogue: row sums over the four lane groups, normalise, store -------
   l_run += __shfl_xor(l_run, 16, 64);
   l_run = halves_sum(l_run);
+  if (nchunks > 1) {
+    // One chunk of a split query block: normalised partial and LSE of row
+    // (wave, query column) for prefill_combine_kernel.
+    const int64_t slot = ((int64_t)kvh * nqb + qblk) * p.max_chunks + chunk;
+    const int row = wave * kQ8 + i16;
+    float* prow = p.part + (slot * kRows8 + row) * D;
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) {
+      const int d = dt * 16 + g4 * 4;
+      *reinterpret_cast<float4*>(prow + d) =
+          float4{oacc[dt][0] * inv, oacc[dt][1] * inv, oacc[dt][2] * inv, oacc[dt][3] * inv};
+    }
+    if (g4 == 0) p.lse[slot * kRows8 + row] = l_run > 0.f ? fast_log2(l_run) + m_ref : -INFINITY;
+    return;
+  }
   if (q0 < S && my_q < S) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
     const int64_t orow = (int64_t)my_q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
@@ -376,6 +404,113 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   }
 }
 
+
+// LSE merge of the chunks of split query blocks (the combine of the
+// reference's split decode, attention.py:168-189, applied per query row):
+// out = sum_c 2^(lse_c - m) part_c / sum_c 2^(lse_c - m).  Work-group
+// (query block, kv head, z) merges 256 consecutive (row, 4 columns) items;
+// each thread issues the loads of up to 8 chunks before it adds them.  Query
+// blocks with a single chunk were written directly by the main kernel.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
+  constexpr int kD4 = D / 4;
+  constexpr int kRowsPerGroup = 256 / kD4;  // rows whose items one work-group merges
+  __shared__ float wts[kMaxChunks][kRowsPerGroup];
+  const int G = p.group;
+  const int pos_per_wg = kQ8 * (kWaves8 / G);
+  const int S = p.seqlen;
+  const int nqb = (S + pos_per_wg - 1) / pos_per_wg;
+  const int qblk = nqb - 1 - (int)blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int wg_q0 = qblk * pos_per_wg;
+  const int wg_qend = min(S, wg_q0 + pos_per_wg);
+  const int nkb = (p.q_offset + wg_qend + kKB8 - 1) / kKB8;
+  const int nchunks = (nkb + p.kb_chunk - 1) / p.kb_chunk;
+  if (nchunks <= 1) return;
+  const int64_t slot0 = ((int64_t)kvh * nqb + qblk) * p.max_chunks;
+  const int t = threadIdx.x;
+  const int row0 = (int)blockIdx.z * kRowsPerGroup;
+  if (t < kRowsPerGroup) {
+    const int row = row0 + t;
+    float m = -INFINITY;
+    for (int c = 0; c < nchunks; ++c) m = fmaxf(m, p.lse[(slot0 + c) * kRows8 + row]);
+    const float m_use = m == -INFINITY ? 0.f : m;
+    float sum = 0.f;
+    for (int c = 0; c < nchunks; ++c) {
+      const float l = p.lse[(slot0 + c) * kRows8 + row];
+      const float w = l == -INFINITY ? 0.f : fast_exp2(l - m_use);
+      wts[c][t] = w;
+      sum += w;
+    }
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    for (int c = 0; c < nchunks; ++c) wts[c][t] *= inv;
+  }
+  __syncthreads();
+  const int lrow = t / kD4;
+  const int row = row0 + lrow;
+  const int d = (t % kD4) * 4;
+  const int w = row / kQ8;
+  const int q = wg_q0 + (w / G) * kQ8 + (row % kQ8);
+  if (q >= S) return;
+  const float* base = p.part + (slot0 * kRows8 + row) * D + d;
+  const int64_t cstride = (int64_t)kRows8 * D;  // floats between chunks of one row
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < nchunks; c0 += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      v[j] = (c0 + j < nchunks && wts[c0 + j][lrow] != 0.f)  // an empty chunk's partial is never read
+                 ? *reinterpret_cast<const float4*>(base + (c0 + j) * cstride)
+                 : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float wc = c0 + j < nchunks ? wts[c0 + j][lrow] : 0.f;
+      acc.x += wc * v[j].x; acc.y += wc * v[j].y; acc.z += wc * v[j].z; acc.w += wc * v[j].w;
+    }
+  }
+  const int head = kvh * G + w % G;
+  const int64_t orow = (int64_t)q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
+  if (p.out_bf16) {
+    const u32x2 pk2 = {pack2(f32_to_bf16_bits(acc.x), f32_to_bf16_bits(acc.y)),
+                       pack2(f32_to_bf16_bits(acc.z), f32_to_bf16_bits(acc.w))};
+    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
+  } else {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = acc;
+  }
+}
+
+PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv_heads, int head_dim, int num_cus) {
+  PrefillSplitPlan plan;
+  const int pos_per_wg = kQ8 * (kWaves8 / group);
+  const int nqb = (seqlen + pos_per_wg - 1) / pos_per_wg;
+  plan.query_blocks = nqb;
+  // Split only grids far smaller than the chip: from a quarter of the CUs up,
+  // the per-chunk prologues, partial writes and the merge cost more than the
+  // shorter chains save (measured at config 4, S = 2048: 72.7 vs 68.5 us).
+  if ((int64_t)nqb * kv_heads * 4 > num_cus) return plan;
+  int64_t total = 0;
+  int nkb_max = 0;
+  for (int qb = 0; qb < nqb; ++qb) {
+    const int qend = min(seqlen, (qb + 1) * pos_per_wg);
+    const int nkb = (q_offset + qend + kKB8 - 1) / kKB8;
+    total += nkb;
+    nkb_max = max(nkb_max, nkb);
+  }
+  total *= kv_heads;
+  // Chunks of ~total / CUs key blocks (one round of work-groups; two rounds
+  // of half the length measured slower), at least two blocks each, at most
+  // kMaxChunks chunks per query block.
+  const int64_t per = (total + (int64_t)num_cus - 1) / (int64_t)num_cus;
+  int chunk = per > 2 ? (int)per : 2;
+  chunk = max(chunk, (nkb_max + kMaxChunks - 1) / kMaxChunks);
+  if (chunk >= nkb_max) return plan;  // no query block would split
+  plan.kb_chunk = chunk;
+  plan.max_chunks = (nkb_max + chunk - 1) / chunk;
+  const size_t rows = (size_t)kv_heads * nqb * plan.max_chunks * kRows8;
+  plan.part_bytes = rows * (size_t)head_dim * 4 + rows * 4;
+  return plan;
+}
+
 bool prefill8_serves(int group, int head_dim) {
   return (group == 1 || group == 2 || group == 4 || group == 8) && (head_dim == 128 || head_dim == 256);
 }
@@ -384,15 +519,20 @@ hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t str
   const int pos_per_wg = kQ8 * (kWaves8 / p.group);
   const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
   const int nblk = (p.q_offset + p.seqlen + kKB8 - 1) / kKB8;
-  const dim3 grid(nqb, p.kv_heads), vt_grid(nblk, p.kv_heads);
+  const bool split = p.kb_chunk > 0;
+  if (split && (p.max_chunks < 1 || p.max_chunks > kMaxChunks || !p.part || !p.lse)) return hipErrorInvalidValue;
+  const dim3 grid(nqb, p.kv_heads, split ? p.max_chunks : 1), vt_grid(nblk, p.kv_heads);
+  const dim3 cgrid(nqb, p.kv_heads, kRows8 * head_dim / 4 / 256);
   switch (head_dim) {
     case 128:
       hipLaunchKernelGGL(prefill_vt8_kernel<128>, vt_grid, dim3(256), 0, stream, p);
       hipLaunchKernelGGL(gqa_prefill8_kernel<128>, grid, dim3(kWaves8 * 64), 0, stream, p);
+      if (split) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
       break;
     case 256:
       hipLaunchKernelGGL(prefill_vt8_kernel<256>, vt_grid, dim3(256), 0, stream, p);
       hipLaunchKernelGGL(gqa_prefill8_kernel<256>, grid, dim3(kWaves8 * 64), 0, stream, p);
+      if (split) hipLaunchKernelGGL(prefill_combine_kernel<256>, cgrid, dim3(256), 0, stream, p);
       break;
     default: return hipErrorInvalidValue;
   }

@@ -131,6 +131,17 @@ int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, c
  * scratch internally. */
 int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t head_dim);
 
+/* Bytes of prefill workspace that also hold the split-key partials: with at
+ * least this much, bt_gqa_prefill splits the key range of long query blocks
+ * across work-groups whenever one work-group per query block would leave
+ * compute units idle (short prompts, long cached prefixes), and merges the
+ * chunks by their LSEs.  Equal to bt_prefill_workspace_bytes(q_offset +
+ * seqlen, ...) when the shape needs no split; 0 for invalid arguments.
+ * Depends on the current device's CU count.  No counterpart in the reference,
+ * whose SDPA call (prefill.py:60-68) sizes its scratch internally. */
+int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32_t heads,
+                                         int32_t kv_heads, int32_t head_dim);
+
 /* Causal GQA prefill attention on bf16 MFMA.  Replaces the
  * F.scaled_dot_product_attention(is_causal=True, enable_gqa=True) call of
  * _prefill_attn (breezetoken/model/prefill.py:56-68; q_offset = 0) and the
@@ -141,8 +152,9 @@ int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t hea
  * (token-major or head-major caches both fit): the cache including the new
  * tokens.  Query row i attends keys 0 .. q_offset + i.  out (seqlen, heads, D)
  * f32 or bf16.  `workspace` (16-byte aligned) must hold
- * bt_prefill_workspace_bytes(q_offset + seqlen, kv_heads, head_dim) bytes; it
- * is scratch for the duration of the call on `stream`. */
+ * bt_prefill_workspace_bytes(q_offset + seqlen, kv_heads, head_dim) bytes, and
+ * bt_prefill_split_workspace_bytes(...) bytes for the split-key schedule; it is
+ * scratch for the duration of the call on `stream`. */
 int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
                    int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
                    int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,

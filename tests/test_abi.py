@@ -60,6 +60,10 @@ def test_workspace_bytes():
     assert lib.bt_prefill_workspace_bytes(8192, 2, 256) == 2 * 8192 * 256 * 2
     assert lib.bt_prefill_workspace_bytes(65, 1, 128) == 128 * 128 * 2
     assert lib.bt_prefill_workspace_bytes(0, 1, 128) == 0
+    # the split-key size refuses the same malformed shapes (before any device query)
+    assert lib.bt_prefill_split_workspace_bytes(0, 0, 8, 2, 256) == 0
+    assert lib.bt_prefill_split_workspace_bytes(16, -1, 8, 2, 256) == 0
+    assert lib.bt_prefill_split_workspace_bytes(16, 0, 6, 4, 256) == 0
 
 
 @pytest.mark.parametrize(

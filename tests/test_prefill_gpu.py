@@ -155,6 +155,62 @@ def test_chunked_prefill_other_group_sizes(hip_backend, heads, kv, dim, steps, p
     _close(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, q_offset=pos0), ref)
 
 
+def _prefill_with_workspace(q, k, v, scale, q_offset, ws_bytes):
+    """bt_gqa_prefill with a workspace of exactly ``ws_bytes`` (f32 output)."""
+    import ctypes
+
+    from breezetoken_amd import _lib
+
+    steps, heads, dim = q.shape
+    out = torch.empty((steps, heads, dim), dtype=torch.float32, device="cuda")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    rc = _lib.lib().bt_gqa_prefill(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+        steps, q_offset, heads, k.shape[1], dim, float(scale), ws.data_ptr(), ws_bytes, out.data_ptr(),
+        _lib.BT_DTYPE_F32, out.stride(0), out.stride(1),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check("bt_gqa_prefill", rc)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("heads,kv,steps,pos0", [(8, 2, 512, 0), (8, 2, 256, 4096), (16, 2, 128, 5000),
+                                                 (8, 2, 300, 1000), (4, 4, 200, 0)])
+def test_split_key_schedule_matches_unsplit(hip_backend, heads, kv, steps, pos0):
+    """Short prompts and long cached prefixes split the key range over several
+    work-groups when the workspace holds the partials; the LSE merge of the
+    chunks equals the one-work-group-per-query-block schedule and the oracle."""
+    from breezetoken_amd import _lib
+
+    lib = _lib.lib()
+    g = torch.Generator().manual_seed(steps + pos0 + heads)
+    q = torch.randn(steps, heads, 256, generator=g).to(torch.bfloat16)
+    k = torch.randn(pos0 + steps, kv, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(pos0 + steps, kv, 256, generator=g).to(torch.bfloat16)
+    scale = 256**-0.5
+    vt_only = lib.bt_prefill_workspace_bytes(pos0 + steps, kv, 256)
+    split = lib.bt_prefill_split_workspace_bytes(steps, pos0, heads, kv, 256)
+    print(f"[split] H={heads} Hkv={kv} S={steps} pos0={pos0} ws {vt_only} -> {split}", flush=True)
+    assert split > vt_only  # these shapes leave CUs idle with one work-group per query block
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    unsplit = _prefill_with_workspace(qd, kd, vd, scale, pos0, vt_only)
+    chunked = _prefill_with_workspace(qd, kd, vd, scale, pos0, split)
+    ref = orc.torch_prefill_banded(q.float(), k.float(), v.float(), pos0, scale)
+    _close(unsplit, ref)
+    _close(chunked, ref)
+    assert (chunked - unsplit).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize("steps", [2048, 8192])
+def test_long_prompt_needs_no_split(hip_backend, steps):
+    """Config 4 at S = 2048 / 8192 has at least a query block per two / one CU:
+    no split (and no extra workspace)."""
+    from breezetoken_amd import _lib
+
+    lib = _lib.lib()
+    assert lib.bt_prefill_split_workspace_bytes(steps, 0, 8, 2, 256) == lib.bt_prefill_workspace_bytes(steps, 2, 256)
+
+
 def test_chunked_prefill_head_major_cache(hip_backend):
     """The SDPA call of qwen36_moe.py:415-423 on views of a head-major
     (Hkv, capacity, D) cache, and the chunks together equal one full prefill."""
