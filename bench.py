@@ -343,6 +343,25 @@ def main() -> int:
                 "kernels": "prefill_vt8_kernel<256> + gqa_prefill8_kernel<256>",
                 "algorithmic_flops": wl.prefill_flops(big["steps"], 8, 256)}
         log("c4: " + json.dumps(pre))
+        # chunked prefill at a cached prefix (qwen36_moe.py:394-428) and a short prompt:
+        # the split-key schedule against one work-group per query block, same process
+        chunked = []
+        for heads, steps, pos0 in ((16, 128, 8192), (16, 512, 16384), (8, 256, 4096), (8, 512, 0)):
+            g = torch.Generator(device=dev).manual_seed(7)
+            qc = torch.randn(steps, heads, 256, generator=g, device=dev).to(torch.bfloat16)
+            kc = torch.randn(pos0 + steps, 2, 256, generator=g, device=dev).to(torch.bfloat16)
+            vc = torch.randn(pos0 + steps, 2, 256, generator=g, device=dev).to(torch.bfloat16)
+            row = {"heads": heads, "kv_heads": 2, "steps": steps, "q_offset": pos0}
+            for key, split in (("us_split", True), ("us_unsplit", False)):
+                row[key] = 1e3 * time_graph(
+                    torch, lambda: backend.attention_prefill(qc, kc, vc, 256**-0.5, torch.bfloat16,
+                                                             q_offset=pos0, split_keys=split),
+                    max(20, esteps // 10), 5)
+            fl = 2 * heads * 256 * steps * (steps + 2 * pos0 + 1)
+            row["TFLOPs_split"] = fl / (row["us_split"] * 1e-6) / 1e12
+            chunked.append(row)
+        extra["chunked_prefill"] = chunked
+        log("chunked prefill: " + json.dumps(chunked))
         # decode-step preparation (q/k RMSNorm + RoPE + bf16 cache writes, layers.py:58-73)
         # for six layers: one fused launch each vs the reference's six-launch decomposition
         # (rms_norm x2, rope x2, index_copy_ x2) on the same HIP operators.

@@ -319,13 +319,15 @@ class HipBackend:
     # ------------------------------------------------------------------ prefill
     def attention_prefill(
         self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
-        out_dtype: torch.dtype = torch.float32, q_offset: int = 0,
+        out_dtype: torch.dtype = torch.float32, q_offset: int = 0, split_keys: bool = True,
     ) -> torch.Tensor:
         """Causal GQA prefill: q (S, H, D) are the new tokens at positions
         q_offset .. q_offset + S - 1, k/v (q_offset + S, Hkv, D) the cache including
         them (any token/head strides), all bf16 -> (S, H, D); row i attends keys
         0 .. q_offset + i.  q_offset = 0 is the SDPA call of prefill.py:56-68, a
-        positive one the banded-mask chunked prefill of qwen36_moe.py:394-428."""
+        positive one the banded-mask chunked prefill of qwen36_moe.py:394-428.
+        ``split_keys=False`` hands the library only the V^T workspace, which keeps
+        one work-group per query block (for comparisons; results agree to ~1e-6)."""
         if q.ndim != 3 or k.ndim != 3 or v.shape != k.shape:
             raise ValueError("prefill expects q (S, H, D), k/v (q_offset + S, Hkv, D)")
         steps, heads, dim = q.shape
@@ -344,10 +346,13 @@ class HipBackend:
             raise RuntimeError("k and v need identical strides")
         out = torch.empty((steps, heads, dim), dtype=out_dtype, device=self._dev)
         ws = self._prefill_workspace(steps, q_offset, heads, groups, dim)
+        ws_len = ws.numel()
+        if not split_keys:
+            ws_len = int(self._lib.bt_prefill_workspace_bytes(q_offset + steps, groups, dim))
         rc = self._lib.bt_gqa_prefill(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1),
             k.stride(0), k.stride(1), steps, q_offset, heads, groups, dim, float(scale),
-            ws.data_ptr(), ws.numel(), out.data_ptr(), _dtype_code(out_dtype),
+            ws.data_ptr(), ws_len, out.data_ptr(), _dtype_code(out_dtype),
             out.stride(0), out.stride(1),
             _stream(self._dev),
         )

@@ -201,6 +201,25 @@ def test_split_key_schedule_matches_unsplit(hip_backend, heads, kv, steps, pos0)
     assert (chunked - unsplit).abs().max().item() <= 1e-3
 
 
+def test_backend_split_keys_switch(hip_backend):
+    """HipBackend.attention_prefill splits by default where the plan does, and
+    split_keys=False keeps one work-group per query block; both match the oracle."""
+    steps, pos0 = 64, 3000
+    g = torch.Generator().manual_seed(41)
+    q = torch.randn(steps, 16, 256, generator=g).to(torch.bfloat16)
+    k = torch.randn(pos0 + steps, 2, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(pos0 + steps, 2, 256, generator=g).to(torch.bfloat16)
+    scale = 256**-0.5
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    split = hip_backend.attention_prefill(qd, kd, vd, scale, q_offset=pos0)
+    one = hip_backend.attention_prefill(qd, kd, vd, scale, q_offset=pos0, split_keys=False)
+    torch.cuda.synchronize()
+    ref = orc.torch_prefill_banded(q.float(), k.float(), v.float(), pos0, scale)
+    _close(split, ref)
+    _close(one, ref)
+    assert (split - one).abs().max().item() <= 1e-3
+
+
 @pytest.mark.parametrize("steps", [2048, 8192])
 def test_long_prompt_needs_no_split(hip_backend, steps):
     """Config 4 at S = 2048 / 8192 has at least a query block per two / one CU:
