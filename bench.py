@@ -346,7 +346,7 @@ def main() -> int:
         # chunked prefill at a cached prefix (qwen36_moe.py:394-428) and a short prompt:
         # the split-key schedule against one work-group per query block, same process
         chunked = []
-        for heads, steps, pos0 in ((16, 128, 8192), (16, 512, 16384), (8, 256, 4096), (8, 512, 0)):
+        for heads, steps, pos0 in ((16, 128, 8192), (16, 512, 16384), (8, 256, 4096), (8, 512, 0), (8, 2048, 0)):
             g = torch.Generator(device=dev).manual_seed(7)
             qc = torch.randn(steps, heads, 256, generator=g, device=dev).to(torch.bfloat16)
             kc = torch.randn(pos0 + steps, 2, 256, generator=g, device=dev).to(torch.bfloat16)

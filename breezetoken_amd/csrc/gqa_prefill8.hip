@@ -484,28 +484,27 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
   const int pos_per_wg = kQ8 * (kWaves8 / group);
   const int nqb = (seqlen + pos_per_wg - 1) / pos_per_wg;
   plan.query_blocks = nqb;
-  // Split only grids far smaller than the chip: from a quarter of the CUs up,
-  // the per-chunk prologues, partial writes and the merge cost more than the
-  // shorter chains save (measured at config 4, S = 2048: 72.7 vs 68.5 us).
-  if ((int64_t)nqb * kv_heads * 4 > num_cus) return plan;
-  int64_t total = 0;
+  // A grid with a work-group per CU or more is already balanced by the
+  // heavy-first launch order.
+  if ((int64_t)nqb * kv_heads >= num_cus) return plan;
   int nkb_max = 0;
   for (int qb = 0; qb < nqb; ++qb) {
     const int qend = min(seqlen, (qb + 1) * pos_per_wg);
-    const int nkb = (q_offset + qend + kKB8 - 1) / kKB8;
-    total += nkb;
-    nkb_max = max(nkb_max, nkb);
+    nkb_max = max(nkb_max, (q_offset + qend + kKB8 - 1) / kKB8);
   }
-  total *= kv_heads;
-  // Chunks of ~total / CUs key blocks (one round of work-groups; two rounds
-  // of half the length measured slower), at least two blocks each, at most
-  // kMaxChunks chunks per query block.
-  const int64_t per = (total + (int64_t)num_cus - 1) / (int64_t)num_cus;
-  int chunk = per > 2 ? (int)per : 2;
-  chunk = max(chunk, (nkb_max + kMaxChunks - 1) / kMaxChunks);
-  if (chunk >= nkb_max) return plan;  // no query block would split
-  plan.kb_chunk = chunk;
-  plan.max_chunks = (nkb_max + chunk - 1) / chunk;
+  // The grid (query blocks x kv heads x max_chunks) must fit the CUs in one
+  // round, counting the slots of chunks that start past a query block's keys
+  // and exit at once: at config 4, S = 1024, 3-block chunks (384 slots) took
+  // 45.5 us against 34.4 us for 4-block chunks (256 slots) and 44.2 us unsplit;
+  // at S = 2048, 16-block chunks (256 slots) took 54.7 us against 62.9 us for
+  // 11-block chunks (384 slots) and 71.5 us unsplit.  Chunks are at least two
+  // key blocks long and a query block has at most kMaxChunks of them.
+  const int slots = num_cus / (nqb * kv_heads);
+  const int max_chunks = min(slots, kMaxChunks);
+  int lo = max(2, (nkb_max + max_chunks - 1) / max_chunks);
+  if (lo >= nkb_max) return plan;  // no query block would split
+  plan.kb_chunk = lo;
+  plan.max_chunks = (nkb_max + lo - 1) / lo;
   const size_t rows = (size_t)kv_heads * nqb * plan.max_chunks * kRows8;
   plan.part_bytes = rows * (size_t)head_dim * 4 + rows * 4;
   return plan;
