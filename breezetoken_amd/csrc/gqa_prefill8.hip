@@ -415,7 +415,7 @@ template <int D>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
   constexpr int kD4 = D / 4;
   constexpr int kRowsPerGroup = 256 / kD4;  // rows whose items one work-group merges
-  __shared__ float wts[kMaxChunks][kRowsPerGroup];
+  constexpr int kBatch = 8;                 // chunks whose loads are in flight together
   const int G = p.group;
   const int pos_per_wg = kQ8 * (kWaves8 / G);
   const int S = p.seqlen;
@@ -429,45 +429,49 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
   if (nchunks <= 1) return;
   const int64_t slot0 = ((int64_t)kvh * nqb + qblk) * p.max_chunks;
   const int t = threadIdx.x;
-  const int row0 = (int)blockIdx.z * kRowsPerGroup;
-  if (t < kRowsPerGroup) {
-    const int row = row0 + t;
-    float m = -INFINITY;
-    for (int c = 0; c < nchunks; ++c) m = fmaxf(m, p.lse[(slot0 + c) * kRows8 + row]);
-    const float m_use = m == -INFINITY ? 0.f : m;
-    float sum = 0.f;
-    for (int c = 0; c < nchunks; ++c) {
-      const float l = p.lse[(slot0 + c) * kRows8 + row];
-      const float w = l == -INFINITY ? 0.f : fast_exp2(l - m_use);
-      wts[c][t] = w;
-      sum += w;
-    }
-    const float inv = sum > 0.f ? 1.f / sum : 0.f;
-    for (int c = 0; c < nchunks; ++c) wts[c][t] *= inv;
-  }
-  __syncthreads();
-  const int lrow = t / kD4;
-  const int row = row0 + lrow;
+  const int row = (int)blockIdx.z * kRowsPerGroup + t / kD4;
   const int d = (t % kD4) * 4;
   const int w = row / kQ8;
   const int q = wg_q0 + (w / G) * kQ8 + (row % kQ8);
   if (q >= S) return;
+  const float* lse = p.lse + slot0 * kRows8 + row;
   const float* base = p.part + (slot0 * kRows8 + row) * D + d;
   const int64_t cstride = (int64_t)kRows8 * D;  // floats between chunks of one row
+  // Every thread loads its row's LSEs and partial slices of a batch of chunks
+  // at once (one memory round trip per batch) and merges online across
+  // batches.  A chunk without keys for the row has lse = -inf: its slice is
+  // selected away, never multiplied (the slice of a chunk that exited early
+  // was never written).
+  float m = -INFINITY, sum = 0.f;
   float4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int c0 = 0; c0 < nchunks; c0 += 8) {
-    float4 v[8];
+  for (int c0 = 0; c0 < nchunks; c0 += kBatch) {
+    float l[kBatch];
+    float4 v[kBatch];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      v[j] = (c0 + j < nchunks && wts[c0 + j][lrow] != 0.f)  // an empty chunk's partial is never read
-                 ? *reinterpret_cast<const float4*>(base + (c0 + j) * cstride)
-                 : float4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float wc = c0 + j < nchunks ? wts[c0 + j][lrow] : 0.f;
-      acc.x += wc * v[j].x; acc.y += wc * v[j].y; acc.z += wc * v[j].z; acc.w += wc * v[j].w;
+    for (int j = 0; j < kBatch; ++j) {
+      const bool in = c0 + j < nchunks;
+      l[j] = in ? lse[(int64_t)(c0 + j) * kRows8] : -INFINITY;
+      v[j] = in ? *reinterpret_cast<const float4*>(base + (c0 + j) * cstride) : float4{0.f, 0.f, 0.f, 0.f};
     }
+    float mb = m;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, l[j]);
+    if (mb == -INFINITY) continue;  // no keys yet for this row
+    const float r = fast_exp2(m - mb);  // m = -inf before the first keys: r = 0
+    sum *= r;
+    acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (l[j] != -INFINITY) {
+        const float wc = fast_exp2(l[j] - mb);
+        sum += wc;
+        acc.x += wc * v[j].x; acc.y += wc * v[j].y; acc.z += wc * v[j].z; acc.w += wc * v[j].w;
+      }
+    }
+    m = mb;
   }
+  const float inv = sum > 0.f ? 1.f / sum : 0.f;
+  acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
   const int head = kvh * G + w % G;
   const int64_t orow = (int64_t)q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
   if (p.out_bf16) {
