@@ -134,6 +134,37 @@ def prefill_mode(torch, backend, dev, calls: int) -> int:
     return 0
 
 
+CHUNKED_CASES = ((16, 128, 8192), (16, 512, 16384), (8, 256, 4096), (8, 512, 0), (8, 2048, 0))
+
+
+def chunked_inputs(torch, dev, heads: int, steps: int, pos0: int):
+    """Seeded q (S, H, 256) and k/v (pos0 + S, 2, 256) bf16 on ``dev``."""
+    g = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(steps, heads, 256, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(pos0 + steps, 2, 256, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(pos0 + steps, 2, 256, generator=g, device=dev).to(torch.bfloat16)
+    return q, k, v
+
+
+def chunked_mode(torch, backend, dev, calls: int) -> int:
+    """Split-key prefill only (for rocprofv3 kernel traces): ``calls`` eager
+    calls of each CHUNKED_CASES shape after two warm-up calls, in that order."""
+    for heads, steps, pos0 in CHUNKED_CASES:
+        q, k, v = chunked_inputs(torch, dev, heads, steps, pos0)
+        for _ in range(2):
+            backend.attention_prefill(q, k, v, 256**-0.5, torch.bfloat16, q_offset=pos0)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(torch.cuda.current_stream())
+        for _ in range(calls):
+            backend.attention_prefill(q, k, v, 256**-0.5, torch.bfloat16, q_offset=pos0)
+        end.record(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "chunked", "heads": heads, "steps": steps, "q_offset": pos0, "calls": calls,
+                          "us_per_call_eager": round(start.elapsed_time(end) * 1e3 / calls, 2)}), flush=True)
+    return 0
+
+
 def ragged_mode(torch, backend, dev, calls: int) -> int:
     """Config-5 ragged decode only (for rocprofv3 kernel traces): ``calls`` calls
     over three copies of the cache after two warm-up calls, timed with HIP events
@@ -174,11 +205,12 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "ragged"], default="bench",
+    ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "ragged", "chunked"], default="bench",
                     help="pmc: only a 256 MiB device copy and the config-2 split kernel, "
                          "5 launches each, for rocprofv3 --pmc runs; prefill: only config-4 "
                          "prefill at S=8192 (--steps calls), for kernel traces; ragged: only "
-                         "config-5 ragged decode (--steps calls), for kernel traces")
+                         "config-5 ragged decode (--steps calls), for kernel traces; chunked: "
+                         "only the split-key prefill shapes (--steps calls each), for kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
         print("this build measures one GPU only: the decode/prefill kernels run on a single "
@@ -206,6 +238,8 @@ def main() -> int:
         return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)))
     if args.mode == "ragged":
         return ragged_mode(torch, backend, dev, max(1, min(args.steps, 500)))
+    if args.mode == "chunked":
+        return chunked_mode(torch, backend, dev, max(1, min(args.steps, 200)))
 
     def fixed_case(case, cap):
         cache = KVCache(cap, case.k.shape[1], case.k.shape[2], dev)
@@ -346,11 +380,8 @@ def main() -> int:
         # chunked prefill at a cached prefix (qwen36_moe.py:394-428) and a short prompt:
         # the split-key schedule against one work-group per query block, same process
         chunked = []
-        for heads, steps, pos0 in ((16, 128, 8192), (16, 512, 16384), (8, 256, 4096), (8, 512, 0), (8, 2048, 0)):
-            g = torch.Generator(device=dev).manual_seed(7)
-            qc = torch.randn(steps, heads, 256, generator=g, device=dev).to(torch.bfloat16)
-            kc = torch.randn(pos0 + steps, 2, 256, generator=g, device=dev).to(torch.bfloat16)
-            vc = torch.randn(pos0 + steps, 2, 256, generator=g, device=dev).to(torch.bfloat16)
+        for heads, steps, pos0 in CHUNKED_CASES:
+            qc, kc, vc = chunked_inputs(torch, dev, heads, steps, pos0)
             row = {"heads": heads, "kv_heads": 2, "steps": steps, "q_offset": pos0}
             for key, split in (("us_split", True), ("us_unsplit", False)):
                 row[key] = 1e3 * time_graph(
