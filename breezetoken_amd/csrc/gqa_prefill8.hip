@@ -96,6 +96,12 @@ __global__ __launch_bounds__(256) void prefill_vt8_kernel(PrefillParams p) {
   const __amdgpu_buffer_rsrc_t vrs =
       rsrc8(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)(p.q_offset + p.seqlen) * row_bytes);
   uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kKB8 * D;
+  // The block's image (8 chunks x D rows x 16 bytes) is assembled in LDS and
+  // stored linearly, 1 KiB per wave instruction; a thread's own 8 output rows
+  // are 128 contiguous bytes, so storing them directly would touch 64 cache
+  // lines per instruction.  16-byte unit x sits in LDS slot x ^ ((x >> 3) & 7).
+  constexpr int kUnits = kKB8 * D * 2 / 16;
+  __shared__ __attribute__((aligned(16))) u32x4 stage[kUnits];
   for (int item = threadIdx.x; item < 8 * kDC; item += 256) {
     const int c = item / kDC, dc = item % kDC;
     u32x4 rows[8];
@@ -114,9 +120,13 @@ __global__ __launch_bounds__(256) void prefill_vt8_kernel(PrefillParams p) {
         const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
         o[m] = pack_rtz8(f0, f1);
       }
-      *reinterpret_cast<u32x4*>(img + ((size_t)c * D + dc * 8 + i) * 8) = o;
+      const int x = c * D + dc * 8 + i;
+      stage[x ^ ((x >> 3) & 7)] = o;
     }
   }
+  __syncthreads();
+  u32x4* dst = reinterpret_cast<u32x4*>(img);
+  for (int x = threadIdx.x; x < kUnits; x += 256) dst[x] = stage[x ^ ((x >> 3) & 7)];
 }
 
 template <int D>
