@@ -126,6 +126,11 @@ __global__ __launch_bounds__(256) void prefill_vt_kernel(PrefillParams p) {
   const __amdgpu_buffer_rsrc_t vrs =
       make_rsrc(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)(p.q_offset + p.seqlen) * row_bytes);
   uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kKB * D;
+  // The block's image is assembled in LDS and stored linearly (1 KiB per wave
+  // instruction) instead of as each thread's 128 contiguous bytes; 16-byte
+  // unit x sits in LDS slot x ^ ((x >> 3) & 7), conflict-free both ways.
+  constexpr int kUnits = kKB * D * 2 / 16;
+  __shared__ __attribute__((aligned(16))) u32x4 stage[kUnits];
   for (int item = threadIdx.x; item < 8 * kDC; item += 256) {
     const int c = item / kDC, dc = item % kDC;
     u32x4 rows[8];
@@ -144,9 +149,13 @@ __global__ __launch_bounds__(256) void prefill_vt_kernel(PrefillParams p) {
         const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
         o[m] = pack_f16_rtz(f0, f1);
       }
-      *reinterpret_cast<u32x4*>(img + ((size_t)c * D + dc * 8 + i) * 8) = o;
+      const int x = c * D + dc * 8 + i;
+      stage[x ^ ((x >> 3) & 7)] = o;
     }
   }
+  __syncthreads();
+  u32x4* dst = reinterpret_cast<u32x4*>(img);
+  for (int x = threadIdx.x; x < kUnits; x += 256) dst[x] = stage[x ^ ((x >> 3) & 7)];
 }
 
 // D: head dim (128 or 256).  Wave w of a work-group handles query head
