@@ -248,3 +248,38 @@ def test_gemv_refuses_bad_arguments_and_sizes_its_workspace():
     assert lib.bt_gemv_bf16(fake, fake + 8, 1024, 1024, 1024, fake, fake, 1 << 30, None) == _lib.BT_EINVAL
     assert lib.bt_gemv_bf16(fake, fake, 1024, 1024, 1024, fake, None, 0, None) == _lib.BT_ENOSPC
     assert lib.bt_gemv_bf16(fake, fake, 1 << 20, 4096, 1024, fake, fake, 1 << 30, None) == _lib.BT_ENOTSUP
+
+
+@pytest.mark.parametrize(
+    "steps,q_offset,heads,max_chunks",
+    [
+        # grid z of the split launches in the committed kernel trace of these shapes
+        (128, 8192, 16, 15),
+        (512, 16384, 16, 4),
+        (256, 4096, 8, 14),
+        (512, 0, 8, 4),
+        (2048, 0, 8, 2),
+        (1024, 0, 8, 4),
+        # a grid of a work-group per CU or more is not split
+        (4096, 0, 8, 0),
+        (8192, 0, 8, 0),
+    ],
+)
+def test_prefill_split_plan_sizes(steps, q_offset, heads, max_chunks):
+    """The split-key plan on a 256-CU device (the count assumed without a GPU):
+    the workspace is the V^T image plus f32 partials and LSEs of
+    kv_heads x query blocks x max_chunks x 128 rows."""
+    from breezetoken_amd import _lib
+
+    lib = _lib.lib()
+    kv, dim = 2, 256
+    vt = lib.bt_prefill_workspace_bytes(q_offset + steps, kv, dim)
+    assert vt == kv * -(-(q_offset + steps) // 64) * 64 * dim * 2
+    got = lib.bt_prefill_split_workspace_bytes(steps, q_offset, heads, kv, dim)
+    if max_chunks == 0:
+        assert got == vt
+        return
+    positions_per_group = 16 * 8 // (heads // kv)
+    query_blocks = -(-steps // positions_per_group)
+    rows = kv * query_blocks * max_chunks * 128
+    assert got == -(-vt // 256) * 256 + rows * dim * 4 + rows * 4
