@@ -83,7 +83,8 @@ struct PrefillSplitPlan {
   int32_t kb_chunk = 0;    // 0: no split
   int32_t max_chunks = 1;
   int32_t query_blocks = 0;
-  size_t part_bytes = 0;   // partials + LSEs
+  size_t part_rows = 0;    // kv_heads x query_blocks x max_chunks x rows per work-group
+  size_t part_bytes = 0;   // part_rows x (head_dim f32 partials + 1 f32 LSE)
 };
 PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv_heads, int head_dim,
                                      int num_cus);

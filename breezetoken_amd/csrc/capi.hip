@@ -386,8 +386,7 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
       p.kb_chunk = plan.kb_chunk;
       p.max_chunks = plan.max_chunks;
       p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_offset);
-      const size_t rows = (size_t)kv_heads * plan.query_blocks * plan.max_chunks * 128;
-      p.lse = p.part + rows * (size_t)head_dim;
+      p.lse = p.part + plan.part_rows * (size_t)head_dim;
     }
     return hip_rc(bt::launch_prefill8(p, head_dim, (hipStream_t)stream));
   }

@@ -498,6 +498,7 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
   const int pos_per_wg = kQ8 * (kWaves8 / group);
   const int nqb = (seqlen + pos_per_wg - 1) / pos_per_wg;
   plan.query_blocks = nqb;
+  if (nqb < 1 || kv_heads < 1 || num_cus < 1) return plan;
   // A grid with a work-group per CU or more is already balanced by the
   // heavy-first launch order.
   if ((int64_t)nqb * kv_heads >= num_cus) return plan;
@@ -519,8 +520,8 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
   if (lo >= nkb_max) return plan;  // no query block would split
   plan.kb_chunk = lo;
   plan.max_chunks = (nkb_max + lo - 1) / lo;
-  const size_t rows = (size_t)kv_heads * nqb * plan.max_chunks * kRows8;
-  plan.part_bytes = rows * (size_t)head_dim * 4 + rows * 4;
+  plan.part_rows = (size_t)kv_heads * nqb * plan.max_chunks * kRows8;
+  plan.part_bytes = plan.part_rows * ((size_t)head_dim * 4 + 4);
   return plan;
 }
 
