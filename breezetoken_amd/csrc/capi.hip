@@ -76,6 +76,32 @@ inline int hip_rc(hipError_t e) { return e == hipSuccess ? BT_OK : (int)e; }
 
 }  // namespace
 
+namespace {
+
+// Compute units of the current device, cached per device.
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  static int cache[64] = {0};
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
+}
+
+// The split-key plan bt_gqa_prefill uses for this shape on the current device
+// (kb_chunk 0: none), and where its partials start in the workspace.
+bt::PrefillSplitPlan prefill_plan(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
+                                  int32_t head_dim, int64_t* part_offset) {
+  *part_offset = align256((int64_t)bt::prefill_vt_bytes(q_offset + seqlen, kv_heads, head_dim));
+  const int group = heads / kv_heads;
+  if (!bt::prefill8_serves(group, head_dim)) return bt::PrefillSplitPlan{};
+  return bt::prefill8_split_plan(seqlen, q_offset, group, kv_heads, head_dim, device_cus());
+}
+
+}  // namespace
+
 extern "C" {
 
 int bt_version(void) { return 100; }
@@ -290,32 +316,6 @@ int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t hea
   if (kv_len < 1 || kv_heads < 1 || head_dim < 1) return 0;
   return (int64_t)bt::prefill_vt_bytes(kv_len, kv_heads, head_dim);
 }
-
-namespace {
-
-// Compute units of the current device, cached per device.
-int device_cus() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
-  static int cache[64] = {0};
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
-  if (dev >= 0 && dev < 64) cache[dev] = n;
-  return n;
-}
-
-// The split-key plan bt_gqa_prefill uses for this shape on the current device
-// (kb_chunk 0: none), and where its partials start in the workspace.
-bt::PrefillSplitPlan prefill_plan(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
-                                  int32_t head_dim, int64_t* part_offset) {
-  *part_offset = align256((int64_t)bt::prefill_vt_bytes(q_offset + seqlen, kv_heads, head_dim));
-  const int group = heads / kv_heads;
-  if (!bt::prefill8_serves(group, head_dim)) return bt::PrefillSplitPlan{};
-  return bt::prefill8_split_plan(seqlen, q_offset, group, kv_heads, head_dim, device_cus());
-}
-
-}  // namespace
 
 int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
                                          int32_t head_dim) {
