@@ -513,7 +513,8 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
   // 45.5 us against 34.4 us for 4-block chunks (256 slots) and 44.2 us unsplit;
   // at S = 2048, 16-block chunks (256 slots) took 54.7 us against 62.9 us for
   // 11-block chunks (384 slots) and 71.5 us unsplit.  Chunks are at least two
-  // key blocks long and a query block has at most kMaxChunks of them.
+  // key blocks long (one-block chunks: S = 128 24.5 vs 22.3 us, S = 256 23.5
+  // vs 25.2 us, S = 512 unchanged) and a query block has at most kMaxChunks.
   const int slots = num_cus / (nqb * kv_heads);
   const int max_chunks = min(slots, kMaxChunks);
   int lo = max(2, (nkb_max + max_chunks - 1) / max_chunks);
