@@ -535,16 +535,18 @@ __device__ __forceinline__ float wave_max(float x) {
 }  // namespace
 
 // LSE combine (attention.py:168-189).  One wave per (head, sequence,
-// 16-column chunk): lane = (split group lane >> 2, float4 column lane & 3).
+// 8-column chunk): lane = (split group lane >> 1, float4 column lane & 1).
 // Each lane fetches the partials and LSEs of its splits in one batch; the max
-// and the sums over the 16 split groups are lane shuffles, so the kernel makes
+// and the sums over the 32 split groups are lane shuffles, so the kernel makes
 // one memory round trip before its store and has no barrier (splits past the
-// first 16*kPre take a slower second pass).  A 256-thread work-group per
-// 64-column chunk with LDS reductions measured 0.5 us slower per call at
-// config 2 (17.68 vs 17.16 us at 32k, 10.21 vs 9.68 us at 4k).
-template <int D, bool RAGGED>
+// first 32*kPre take a slower second pass).  Per config-2 call at 32k this
+// took 17.05 us, against 17.17 us with 16 groups x 4 columns, 17.18 us with
+// 64 groups x 1 column, and 17.68 us for a 256-thread work-group per
+// 64-column chunk with LDS reductions.
+template <int D, bool RAGGED, int GROUPS>
 __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p) {
-  constexpr int kPre = 8;  // splits per lane fetched up front (16 groups x 8 = 128)
+  constexpr int kCols = 64 / GROUPS;   // float4 columns per wave
+  constexpr int kPre = 128 / GROUPS;   // splits per lane fetched up front (GROUPS x kPre = 128)
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int chunk = blockIdx.z;
@@ -558,15 +560,15 @@ __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p)
     ns = p.num_split;
   }
   const float* lse = p.lse + (int64_t)h * p.total_splits + base;
-  const int c4 = t & 3;   // float4 column inside the 16-column chunk
-  const int sg = t >> 2;  // split group
-  const float* part = p.part + ((int64_t)h * p.total_splits + base) * D + chunk * 16 + c4 * 4;
+  const int c4 = t % kCols;  // float4 column inside the chunk
+  const int sg = t / kCols;  // split group
+  const float* part = p.part + ((int64_t)h * p.total_splits + base) * D + chunk * 4 * kCols + c4 * 4;
 
   float4 pv[kPre];
   float pl[kPre];
 #pragma unroll
   for (int i = 0; i < kPre; ++i) {
-    const int s = sg + 16 * i;
+    const int s = sg + GROUPS * i;
     pl[i] = -INFINITY;
     pv[i] = float4{0.f, 0.f, 0.f, 0.f};
     if (s < ns) {
@@ -577,7 +579,7 @@ __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p)
   float mx = pl[0];
 #pragma unroll
   for (int i = 1; i < kPre; ++i) mx = fmaxf(mx, pl[i]);
-  for (int s = sg + 16 * kPre; s < ns; s += 16) mx = fmaxf(mx, lse[s]);
+  for (int s = sg + GROUPS * kPre; s < ns; s += GROUPS) mx = fmaxf(mx, lse[s]);
   mx = wave_max(mx);
   // Empty splits have lse = -inf: weight 0, and their (never written) partial is skipped.
   const float m_use = mx == -INFINITY ? 0.f : mx;
@@ -592,7 +594,7 @@ __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p)
       acc.x += w * pv[i].x; acc.y += w * pv[i].y; acc.z += w * pv[i].z; acc.w += w * pv[i].w;
     }
   }
-  for (int s = sg + 16 * kPre; s < ns; s += 16) {
+  for (int s = sg + GROUPS * kPre; s < ns; s += GROUPS) {
     const float l = lse[s];
     if (l != -INFINITY) {
       const float w = fast_exp2(l - m_use);
@@ -601,20 +603,20 @@ __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p)
       acc.x += w * v.x; acc.y += w * v.y; acc.z += w * v.z; acc.w += w * v.w;
     }
   }
-  // Sum over the split groups (lane bits 2..5); every float4 column sees the
+  // Sum over the split groups (the lane bits above the column); every float4 column sees the
   // same splits, so each column's wsum is the full weight sum.
 #pragma unroll
-  for (int o = 4; o < 64; o <<= 1) {
+  for (int o = kCols; o < 64; o <<= 1) {
     acc.x += __shfl_xor(acc.x, o, 64);
     acc.y += __shfl_xor(acc.y, o, 64);
     acc.z += __shfl_xor(acc.z, o, 64);
     acc.w += __shfl_xor(acc.w, o, 64);
     wsum += __shfl_xor(wsum, o, 64);
   }
-  if (t < 4) {
+  if (t < kCols) {
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
     acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
-    const int64_t orow = (int64_t)b * p.out_stride_seq + (int64_t)h * D + chunk * 16 + t * 4;
+    const int64_t orow = (int64_t)b * p.out_stride_seq + (int64_t)h * D + chunk * 4 * kCols + t * 4;
     if (p.out_bf16) {
       uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + orow;
       const u32x2 pk = {pack2(f32_to_bf16_bits(acc.x), f32_to_bf16_bits(acc.y)),
@@ -675,21 +677,32 @@ hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int gri
   }
 }
 
+#ifndef BT_COMBINE_RAGGED_GROUPS
+#define BT_COMBINE_RAGGED_GROUPS 8
+#endif
+// Split groups per combine wave: 32 for a uniform split count (up to 128
+// splits per sequence); a ragged batch averages a few splits per sequence, so
+// its waves take fewer groups and more columns (fewer, fuller waves).
+constexpr int kCombineGroups = 32;
+constexpr int kCombineRaggedGroups = BT_COMBINE_RAGGED_GROUPS;
+
 template <int D>
-static void launch_combine_t(const CombineParams& p, dim3 grid, hipStream_t stream) {
-  if (p.split_base != nullptr)
-    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, true>), grid, dim3(64), 0, stream, p);
-  else
-    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, false>), grid, dim3(64), 0, stream, p);
+static void launch_combine_t(const CombineParams& p, int heads, int batch, hipStream_t stream) {
+  if (p.split_base != nullptr) {
+    const dim3 grid(heads, batch, D / (4 * (64 / kCombineRaggedGroups)));
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, true, kCombineRaggedGroups>), grid, dim3(64), 0, stream, p);
+  } else {
+    const dim3 grid(heads, batch, D / (4 * (64 / kCombineGroups)));
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, false, kCombineGroups>), grid, dim3(64), 0, stream, p);
+  }
 }
 
 hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads, int batch,
                                  hipStream_t stream) {
-  dim3 grid(heads, batch, head_dim / 16);
   switch (head_dim) {
-    case 64: launch_combine_t<64>(p, grid, stream); break;
-    case 128: launch_combine_t<128>(p, grid, stream); break;
-    case 256: launch_combine_t<256>(p, grid, stream); break;
+    case 64: launch_combine_t<64>(p, heads, batch, stream); break;
+    case 128: launch_combine_t<128>(p, heads, batch, stream); break;
+    case 256: launch_combine_t<256>(p, heads, batch, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
