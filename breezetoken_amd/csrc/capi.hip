@@ -208,9 +208,21 @@ int bt_gqa_decode(const void* q, int32_t q_dtype, int64_t q_stride_seq, const vo
   float* lse = static_cast<float*>(workspace);
   float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                          align256((int64_t)heads * total * 4));
-  rc = bt_gqa_decode_split(q, q_dtype, q_stride_seq, k, v, kv_stride_tok, kv_stride_head,
-                           seq_offset, pos, seq_len, seqlen, batch, heads, kv_heads, head_dim,
-                           num_split, scale, lse, part, stream);
+  if (!pos && !seq_len && seqlen < 0) return BT_EINVAL;
+  if (pos && seqlen < 1) return BT_EINVAL;  // capacity bound for the position path
+  if (bt::decode_mode(false, pos != nullptr, seq_len != nullptr, seq_offset != nullptr, batch) < 0)
+    return BT_EINVAL;
+  if ((int64_t)seqlen * kv_stride_tok * 2 > (int64_t)UINT32_MAX) return BT_ENOTSUP;
+  bt::DecodeSplitParams p = make_split_params(q, q_dtype, q_stride_seq, k, v, kv_stride_tok,
+                                              kv_stride_head, seq_offset, pos, seq_len, seqlen,
+                                              heads, kv_heads, head_dim, scale, lse, part);
+  p.work = nullptr;
+  p.num_split = num_split;
+  p.total_splits = total;
+  // A short context in a large grid uses fewer, fuller splits (the split count
+  // follows the length on the device; the combine skips the empty splits).
+  p.tiles_per_split = bt::kDecodeTilesPerSplit;
+  rc = hip_rc(bt::launch_decode_split(p, head_dim, num_split, batch, (hipStream_t)stream));
   if (rc) return rc;
   return bt_gqa_decode_combine(lse, part, batch, heads, head_dim, num_split, nullptr, nullptr,
                                total, out, out_dtype, out_stride_seq, stream);

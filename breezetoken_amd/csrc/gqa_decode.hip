@@ -93,48 +93,54 @@ enum DecodeMode : int {
   kModeLenBatch = 4,  // device lengths + first slots, uniform split count
 };
 
-// GMAX: 4 (groups of <= 4 query heads) or 8; D: head dim; WAVES: waves per
-// work-group; TILE: tokens a wave processes per step (16 or 32); PIPE: 1 =
-// one register buffer whose next tile is fetched as soon as it is consumed,
-// P > 1 = P register buffers, all filled at entry and each refilled right
-// after its tile is used (P tiles in flight);
-// MODE: a DecodeMode; QBF16: q is bf16 (else f32).
-template <int GMAX, int D, int WAVES, int TILE, int PIPE, int MODE, bool QBF16>
-__global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeSplitParams p) {
-  constexpr int kThreads = WAVES * 64;
+// Split pass.  GMAX: 4 (groups of <= 4 query heads) or 8; D: head dim; W:
+// waves per work-group; MODE: a DecodeMode; QBF16: q is bf16 (else f32).
+//
+// Tile t (16 tokens) of a sequence belongs to split t % ns_eff and, inside
+// it, to wave (t / ns_eff) % W; a wave's successive tiles are ns_eff * W
+// apart.  ns_eff = min(ns, ceil(tiles / tiles_per_split)) when the launch
+// gives tiles_per_split (single-sequence and uniform-batch modes), else ns: a
+// short context in a large grid then spreads over ceil(tiles / 2) splits
+// instead of leaving most waves of 128 work-groups idle, and the splits past
+// ns_eff write lse = -inf at once.
+//
+// Per tile and wave, K (16 tokens x D) and V land in registers; K feeds the
+// MFMA directly, V is staged through the wave's XOR-swizzled LDS tile and read
+// back transposed.  A wave requests its next K as soon as Q.K^T has consumed
+// the current one and its next V as soon as the current V is in LDS.
+template <int GMAX, int D, int W, int MODE, bool QBF16>
+__global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplitParams p) {
+  constexpr int kThreads = W * 64;
   constexpr int kSteps = D / 32;            // K-dimension steps of Q.K^T
-  constexpr int kSub = TILE / 16;           // 16-token sub-tiles of S^T
   constexpr int kDTiles = D / 16;           // 16-wide d tiles of O^T
   constexpr int kSlots = D / 8;             // 16-byte chunks per row
-  constexpr int kRowBytes = D * 2;
-  constexpr int kVTileBytes = TILE * kRowBytes;
-  constexpr int kVLoads = kVTileBytes / 1024;  // 1 KiB wave loads per V tile
+  constexpr int kRowBytes = D * 2;          // one kv head of one token
+  constexpr int kTileBytes = 16 * kRowBytes;
+  constexpr int kVLoads = kTileBytes / 1024;  // 1 KiB wave loads per V tile
   constexpr int kRowsPerLoad = 1024 / kRowBytes;
-  constexpr int kSwzPeriod = 8 / kRowsPerLoad > 0 ? 8 / kRowsPerLoad : 1;
-  static_assert(TILE == 16 || TILE == 32, "tile is 16 or 32 tokens");
-  static_assert(kVLoads >= 1, "V tile must fill at least one wave load");
+  static_assert(kVLoads >= 1 && kSlots >= 8, "head_dim 64, 128 or 256");
+  static_assert(kSteps <= W, "one wave per d-step builds Q^T");
 
-  // LDS: one V tile per wave, and a separate cross-wave merge area so that a
-  // wave can deposit its partial as soon as its own loop ends (the stores of
-  // the group's waves then spread out in time instead of all queueing behind
-  // one barrier).  Merge rows [wave][head][d] have a stride of D + 4 floats
-  // (= 4 banks mod 64), so the lanes that store one d-tile of different heads
-  // fall on distinct bank groups instead of conflicting on a 1 KiB stride.
+  // LDS: one V tile per wave (16-byte chunk c of token row r in slot c ^
+  // swz(r), so the transposed reads of 16 rows are conflict-free), the
+  // cross-wave merge rows [wave][head][d] with a stride of D + 4 floats (the
+  // lanes that store one d-tile of different heads fall on distinct banks), a
+  // wave deposits its partial as soon as its own loop ends, and the Q^T
+  // operand shared by all waves.
   constexpr int kMoStride = D + 4;
-  constexpr int kMergeFloats = WAVES * GMAX * (kMoStride + 2);
-  constexpr int kVBytes = WAVES * kVTileBytes;
-  static_assert(kVBytes + kMergeFloats * 4 + kSteps * 64 * 16 <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kVBytes];
-  __shared__ __attribute__((aligned(16))) float mlds[kMergeFloats];
-  // Q^T operand, identical for every wave: [step][lane] 16-byte fragments.
-  __shared__ __attribute__((aligned(16))) u32x4 qlds[kSteps * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char vlds[W * kTileBytes];
+  __shared__ __attribute__((aligned(16))) float mlds[W * GMAX * kMoStride];
+  __shared__ __attribute__((aligned(16))) u32x4 qlds[kSteps * 64];  // [step][lane]
+  __shared__ float mstat[2 * W * GMAX];                              // m and l per (wave, head)
+  static_assert(W * kTileBytes + W * GMAX * kMoStride * 4 + kSteps * 1024 + 8 * W * GMAX <= 160 * 1024,
+                "LDS budget");
 
   // Every kernel argument lands in SGPRs in one batch of scalar loads here,
   // instead of lazily inside branches (each lazy batch is a memory round trip).
   asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.v), "s"(p.pos), "s"(p.seq_len), "s"(p.seq_offset),
                "s"(p.work), "s"(p.seqlen), "s"(p.num_split), "s"(p.total_splits), "s"(p.group),
                "s"(p.kv_stride_tok), "s"(p.kv_stride_head), "s"(p.q_stride_seq), "s"(p.scale_log2),
-               "s"(p.lse), "s"(p.part));
+               "s"(p.lse), "s"(p.part), "s"(p.tiles_per_split));
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kvh = blockIdx.y;
@@ -147,8 +153,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
   } else {
     b = blockIdx.z; s = blockIdx.x; ns = p.num_split; base = b * p.num_split;
   }
-  // The length source is read first so its round trip overlaps the q and
-  // K/V loads issued below.
+  // The length source is read first so its round trip overlaps the q loads.
   int len_raw;
   if constexpr (MODE == kModePos || MODE == kModePosBatch) len_raw = uniform_load(p.pos, b) + 1;
   else if constexpr (MODE == kModeRagged || MODE == kModeLenBatch) len_raw = uniform_load(p.seq_len, b);
@@ -174,59 +179,121 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
   const uint32_t keep_hi = (col_head >= 0 && !col_lo) ? 0xffffu : 0u;
   const uint32_t keep_lo = col_lo ? 0xffffu : 0u;
 
-  // ---- wave 0 issues the q loads first: they do not depend on the length ----
+  // ---- q first: wave w < kSteps loads the q slice of d-step w at entry ------
+  // (a wave's loads complete in issue order, so q must not queue behind K/V).
   const int64_t qrow = (int64_t)b * p.q_stride_seq + (int64_t)(head0 + (col_head < 0 ? 0 : col_head)) * D;
-  u32x4 qraw[kSteps][2];
-  if (wave == 0) {
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-      const int d0 = (st * 4 + kg) * 8;
-      if constexpr (QBF16) {
-        qraw[st][0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(p.q) + qrow + d0);
-      } else {
-        qraw[st][0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.q) + qrow + d0);
-        qraw[st][1] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.q) + qrow + d0 + 4);
-      }
+  u32x4 qraw[2];
+  if (wave < kSteps) {
+    const int d0 = (wave * 4 + kg) * 8;
+    if constexpr (QBF16) {
+      qraw[0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(p.q) + qrow + d0);
+    } else {
+      qraw[0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.q) + qrow + d0);
+      qraw[1] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.q) + qrow + d0 + 4);
     }
   }
 
   // ---- K/V addressing -------------------------------------------------------
+  // K: lane (col, kg) holds token col's 16 bytes kg of each 64-byte d-step.
+  // V: load j of a tile fills LDS bytes [1024 j, +1024) of the wave's tile;
+  // lane l fetches the chunk that belongs in its slot (the swizzle is applied
+  // on the source side).
   const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-  unsigned char* vtile = smem + wave * kVTileBytes;
-
-  uint32_t koff[kSub];
-#pragma unroll
-  for (int sub = 0; sub < kSub; ++sub) koff[sub] = (uint32_t)(sub * 16 + col) * row_bytes + kg * 16;
-  uint32_t voff[kSwzPeriod];
-#pragma unroll
-  for (int j = 0; j < kSwzPeriod; ++j) {
+  unsigned char* vtile = vlds + wave * kTileBytes;
+  const uint32_t koff = (uint32_t)col * row_bytes + kg * 16;
+  auto voff = [&](int j) -> uint32_t {
     const int r = j * kRowsPerLoad + lane / kSlots;
-    const int c = (lane % kSlots) ^ swz(r, kSlots);
-    voff[j] = (uint32_t)r * row_bytes + c * 16;
-  }
+    return (uint32_t)(lane / kSlots) * row_bytes + (uint32_t)((lane % kSlots) ^ swz(r, kSlots)) * 16;
+  };
 
   // Speculative path (device position, single sequence): the split's first
-  // tile is tile s, so wave 0 fetches it inside the capacity bound before the
-  // position is known.  Slots in [valid, capacity) are masked after it arrives.
-  constexpr bool speculate = MODE == kModePos;
+  // tile is tile s whatever ns_eff turns out to be, so wave 0 fetches it inside
+  // the capacity bound before the position is known; rows past the valid
+  // length are zeroed once it arrives.
+  constexpr bool kSpec = MODE == kModePos;
   const int64_t head_off0 = (int64_t)kvh * p.kv_stride_head;
   __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + head_off0, (uint32_t)p.seqlen * row_bytes);
   __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.v + head_off0, (uint32_t)p.seqlen * row_bytes);
 
-  auto load_k = [&](int tile, u32x4 (&kr)[kSub][kSteps]) {
-    const uint32_t so = (uint32_t)tile * TILE * row_bytes;
+  u32x4 kr[kSteps];
+  u32x4 vr[kVLoads];
+  auto issue_k = [&](int tile) {
+    const uint32_t so = (uint32_t)tile * 16 * row_bytes;
 #pragma unroll
-    for (int st = 0; st < kSteps; ++st)
-#pragma unroll
-      for (int sub = 0; sub < kSub; ++sub) kr[sub][st] = buf_load16(krs, koff[sub] + st * 64, so);
+    for (int st = 0; st < kSteps; ++st) kr[st] = buf_load16(krs, koff + st * 64, so);
   };
-  auto load_v = [&](int tile, u32x4 (&vr)[kVLoads]) {
-    const uint32_t so = (uint32_t)tile * TILE * row_bytes;
+  auto issue_v = [&](int tile) {
+    const uint32_t so = (uint32_t)tile * 16 * row_bytes;
 #pragma unroll
-    for (int j = 0; j < kVLoads; ++j)
-      vr[j] = buf_load16(vrs, voff[j % kSwzPeriod],
-                         so + (uint32_t)(j / kSwzPeriod) * (kSwzPeriod * kRowsPerLoad) * row_bytes);
+    for (int j = 0; j < kVLoads; ++j) vr[j] = buf_load16(vrs, voff(j), so + (uint32_t)(j * kRowsPerLoad) * row_bytes);
   };
+  const bool spec_loaded = kSpec && wave == 0;
+  if (spec_loaded) {
+    issue_k(s);
+    issue_v(s);
+  }
+
+  // ---- valid length, effective split count, this wave's tiles --------------
+  int valid = len_raw;
+  if constexpr (MODE == kModePos || MODE == kModePosBatch) {
+    if (valid > p.seqlen) valid = p.seqlen;  // seqlen carries the capacity here
+  }
+  if (valid < 0) valid = 0;
+  // From here on loads stop at the valid length: rows past it read as zeros.
+  {
+    const int64_t head_off = seq_off * p.kv_stride_tok + head_off0;
+    krs = make_rsrc(p.k + head_off, (uint32_t)valid * row_bytes);
+    vrs = make_rsrc(p.v + head_off, (uint32_t)valid * row_bytes);
+  }
+  const int tiles = (valid + 15) / 16;
+  int ns_eff = ns;
+  if constexpr (MODE != kModeRagged) {
+    if (p.tiles_per_split > 0) {
+      const int want = (tiles + p.tiles_per_split - 1) / p.tiles_per_split;
+      ns_eff = want < 1 ? 1 : (want < ns ? want : ns);
+    }
+  }
+  if (s >= ns_eff || s >= tiles) {
+    if (threadIdx.x < G) p.lse[(int64_t)(head0 + threadIdx.x) * p.total_splits + split_idx] = -INFINITY;
+    return;
+  }
+  const int tstride = ns_eff * W;                       // tile distance between a wave's steps
+  const int tfirst = s + ns_eff * wave;                 // this wave's first tile
+  const int my_tiles = tfirst < tiles ? (tiles - tfirst + tstride - 1) / tstride : 0;
+  if (my_tiles > 0 && !spec_loaded) {
+    issue_k(tfirst);
+    issue_v(tfirst);
+  }
+
+  // ---- Q^T operand (bf16 hi or lo of q*scale*log2e): wave w builds d-step w.
+  if (wave < kSteps) {
+    float qv[8];
+    if constexpr (QBF16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qv[2 * i] = bf16_bits_to_f32(qraw[0][i] & 0xffffu);
+        qv[2 * i + 1] = bf16_bits_to_f32(qraw[0][i] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qv[i] = __uint_as_float(qraw[0][i]);
+        qv[4 + i] = __uint_as_float(qraw[1][i]);
+      }
+    }
+    uint32_t h16[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = qv[i] * p.scale_log2;
+      const uint32_t hi = f32_to_bf16_bits(x);
+      const uint32_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
+      h16[i] = (hi & keep_hi) | (lo & keep_lo);
+    }
+    qlds[wave * 64 + lane] = u32x4{pack2(h16[0], h16[1]), pack2(h16[2], h16[3]), pack2(h16[4], h16[5]),
+                                   pack2(h16[6], h16[7])};
+  }
+  // Publish Q^T without waiting for the K/V requests in flight (no vmcnt wait).
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   // ---- per-wave state -------------------------------------------------------
   floatx4 oacc[kDTiles];
@@ -234,130 +301,42 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
   for (int i = 0; i < kDTiles; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY;
   float l_run = 0.f;
-
-  u32x4 kr[PIPE][kSub][kSteps];
-  u32x4 vr[PIPE][kVLoads];
-  const bool spec_loaded = speculate && wave == 0;
-  if (spec_loaded) {
-    load_k(s, kr[0]);
-    load_v(s, vr[0]);
-  }
-
-  // ---- valid length (device position, length table or argument) ------------
-  int valid = len_raw;
-  if constexpr (MODE == kModePos || MODE == kModePosBatch) {
-    if (valid > p.seqlen) valid = p.seqlen;  // seqlen carries the capacity here
-  }
-  if (valid < 0) valid = 0;
-  if constexpr (!speculate) {
-    const int64_t head_off = seq_off * p.kv_stride_tok + head_off0;
-    krs = make_rsrc(p.k + head_off, (uint32_t)valid * row_bytes);
-    vrs = make_rsrc(p.v + head_off, (uint32_t)valid * row_bytes);
-  }
-
-  // Round-robin partition: tile t belongs to split t % ns; inside the split,
-  // wave w takes the split's tiles w, w + WAVES, ...
-  const int tiles = (valid + TILE - 1) / TILE;
-  const int n_tiles = tiles > s ? (tiles - s + ns - 1) / ns : 0;
-  if (n_tiles == 0) {
-    if (threadIdx.x < G) p.lse[(int64_t)(head0 + threadIdx.x) * p.total_splits + split_idx] = -INFINITY;
-    return;
-  }
-  const int my_tiles = n_tiles > wave ? (n_tiles - wave + WAVES - 1) / WAVES : 0;
-  const int tstride = ns * WAVES;        // tile distance between a wave's steps
-  const int tfirst = s + ns * wave;      // this wave's first tile
-  if (my_tiles > 0) {
-    if (!spec_loaded) {
-      load_k(tfirst, kr[0]);
-      load_v(tfirst, vr[0]);
-    }
-#pragma unroll
-    for (int b = 1; b < PIPE; ++b) {
-      if (b < my_tiles) {
-        load_k(tfirst + b * tstride, kr[b]);
-        load_v(tfirst + b * tstride, vr[b]);
-      }
-    }
-  }
-
-  // ---- wave 0 builds the Q^T operand (bf16 hi or lo of q*scale*log2e) -------
-  if (wave == 0) {
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-      float qv[8];
-      if constexpr (QBF16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          qv[2 * i] = bf16_bits_to_f32(qraw[st][0][i] & 0xffffu);
-          qv[2 * i + 1] = bf16_bits_to_f32(qraw[st][0][i] >> 16);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          qv[i] = __uint_as_float(qraw[st][0][i]);
-          qv[4 + i] = __uint_as_float(qraw[st][1][i]);
-        }
-      }
-      uint32_t h16[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float x = qv[i] * p.scale_log2;
-        const uint32_t hi = f32_to_bf16_bits(x);
-        const uint32_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
-        h16[i] = (hi & keep_hi) | (lo & keep_lo);
-      }
-      const u32x4 packed = {pack2(h16[0], h16[1]), pack2(h16[2], h16[3]), pack2(h16[4], h16[5]),
-                            pack2(h16[6], h16[7])};
-      qlds[st * 64 + lane] = packed;
-    }
-  }
-  __syncthreads();
-
   const int i16 = lane & 15;
-  auto compute = [&](int tile, bool fetch_next, u32x4 (&k)[kSub][kSteps], u32x4 (&v)[kVLoads]) {
-    // S^T = K . Q^T, one 16-token sub-tile per accumulator.
-    floatx4 sacc[kSub];
-#pragma unroll
-    for (int sub = 0; sub < kSub; ++sub) sacc[sub] = floatx4{0.f, 0.f, 0.f, 0.f};
-    // Re-read Q^T from LDS every tile instead of pinning 32 VGPRs for the whole loop.
-    asm volatile("" ::: "memory");
+  const int row1 = 4 * kg + (i16 >> 2);  // V^T read: token row of this lane
+
+  for (int it = 0; it < my_tiles; ++it) {
+    const int tile = tfirst + it * tstride;
+    const bool more = it + 1 < my_tiles;
+    // S^T = K . Q^T.
+    floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
     u32x4 qop[kSteps];
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) qop[st] = qlds[st * 64 + lane];
 #pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-#pragma unroll
-      for (int sub = 0; sub < kSub; ++sub)
-        sacc[sub] = mfma16(as_bf16x8(k[sub][st]), as_bf16x8(qop[st]), sacc[sub]);
-    }
-    if (PIPE == 1 && fetch_next) load_k(tile + tstride, k);
-    // Stage V into this wave's swizzled LDS tile (same-wave LDS ops stay ordered).
-    // Rows past the valid length become zeros: P is 0 there, but 0 * NaN is not.
+    for (int st = 0; st < kSteps; ++st) sacc = mfma16(as_bf16x8(kr[st]), as_bf16x8(qop[st]), sacc);
+    if (more) issue_k(tile + tstride);
+    // Stage V in this wave's swizzled LDS tile (same-wave LDS ops stay
+    // ordered) and request the next V.  Rows past the valid length are zeros
+    // (buffer range), except in a speculative tile read inside the capacity:
+    // there they are zeroed here, since p = 0 on them but 0 * NaN is not 0.
+    const bool spec_tail = kSpec && it == 0 && spec_loaded && tile * 16 + 16 > valid;
 #pragma unroll
     for (int j = 0; j < kVLoads; ++j) {
-      const int r = (j / kSwzPeriod) * (kSwzPeriod * kRowsPerLoad) + (j % kSwzPeriod) * kRowsPerLoad + lane / kSlots;
       const u32x4 z = {0u, 0u, 0u, 0u};
-      *reinterpret_cast<BT_LDS u32x4*>((BT_LDS unsigned char*)vtile + j * 1024 + lane * 16) =
-          tile * TILE + r < valid ? v[j] : z;
+      const bool dead = spec_tail && tile * 16 + j * kRowsPerLoad + lane / kSlots >= valid;
+      *reinterpret_cast<BT_LDS u32x4*>((BT_LDS unsigned char*)vtile + j * 1024 + lane * 16) = dead ? z : vr[j];
     }
-    if (PIPE == 1 && fetch_next) load_v(tile + tstride, v);
+    if (more) issue_v(tile + tstride);
 
     // hi + lo columns, mask, online softmax (attention.py:21-51 semantics).
-    constexpr int kVals = kSub * 4;
-    float x[kVals];
+    float x[4];
 #pragma unroll
-    for (int sub = 0; sub < kSub; ++sub) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float vv = sacc[sub][j];
-        vv += mirror<GMAX>(vv);
-        const int t = tile * TILE + sub * 16 + kg * 4 + j;
-        x[sub * 4 + j] = t < valid ? vv : -INFINITY;
-      }
+    for (int j = 0; j < 4; ++j) {
+      float vv = sacc[j];
+      vv += mirror<GMAX>(vv);
+      x[j] = tile * 16 + kg * 4 + j < valid ? vv : -INFINITY;
     }
-    float tmax = x[0];
-#pragma unroll
-    for (int i = 1; i < kVals; ++i) tmax = fmaxf(tmax, x[i]);
+    float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
     tmax = wave_max_xor(tmax, 16);
     tmax = wave_max_xor(tmax, 32);
     // Lazy reference max: m_run moves only when a score exceeds it by more
@@ -371,88 +350,35 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
     const float m_new = move ? tmax : m_run;
     const float alpha = move ? fast_exp2(m_run - m_new) : 1.f;  // 0 when m_run is -inf
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    float pr[kVals];
+    float pr[4];
 #pragma unroll
-    for (int i = 0; i < kVals; ++i) pr[i] = fast_exp2(x[i] - m_use);
+    for (int j = 0; j < 4; ++j) pr[j] = fast_exp2(x[j] - m_use);
     m_run = m_new;
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < kVals; ++i) psum += pr[i];
-    l_run = l_run * alpha + psum;
+    l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
     if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
       for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
     }
-
     // P^T operand: this lane's own probabilities, as bf16 hi or lo.
-    uint32_t p16[kVals];
+    uint32_t p16[4];
 #pragma unroll
-    for (int i = 0; i < kVals; ++i) {
-      const uint32_t hi = f32_to_bf16_bits(pr[i]);
-      const uint32_t lo = f32_to_bf16_bits(pr[i] - bf16_bits_to_f32(hi));
-      p16[i] = (hi & keep_hi) | (lo & keep_lo);
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t hi = f32_to_bf16_bits(pr[j]);
+      const uint32_t lo = f32_to_bf16_bits(pr[j] - bf16_bits_to_f32(hi));
+      p16[j] = (hi & keep_hi) | (lo & keep_lo);
     }
+    const u32x2 pop = {pack2(p16[0], p16[1]), pack2(p16[2], p16[3])};
 
     // O^T += V^T . P^T, V^T read transposed from LDS.
-    const int row1 = 4 * kg + (i16 >> 2);
-    if constexpr (TILE == 32) {
-      const u32x4 ppk = {pack2(p16[0], p16[1]), pack2(p16[2], p16[3]), pack2(p16[4], p16[5]),
-                         pack2(p16[6], p16[7])};
-      const bf16x8 pop = as_bf16x8(ppk);
-      const int row2 = row1 + 16;
-      constexpr int kBatch = WAVES <= 4 ? kDTiles : kDTiles / 2;  // reads in flight
+    u32x2 vop[kDTiles];
 #pragma unroll
-      for (int d0 = 0; d0 < kDTiles; d0 += kBatch) {
-        bf16x8 vop[kBatch];
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          const int c = (d0 + i) * 2 + ((i16 & 3) >> 1);
-          const int off = (i16 & 1) * 8;
-          const BT_LDS uint16_t* p0 = (const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row1 * kRowBytes +
-                                                              ((c ^ swz(row1, kSlots)) * 16) + off);
-          const BT_LDS uint16_t* p1 = (const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row2 * kRowBytes +
-                                                              ((c ^ swz(row2, kSlots)) * 16) + off);
-          vop[i] = lds_read_tr_pair(p0, p1);
-        }
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) oacc[d0 + i] = mfma16(vop[i], pop, oacc[d0 + i]);
-      }
-    } else {
-      const u32x2 pop = {pack2(p16[0], p16[1]), pack2(p16[2], p16[3])};
-      u32x2 vop[kDTiles];
-#pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) {
-        const int c = dt * 2 + ((i16 & 3) >> 1);
-        const int off = (i16 & 1) * 8;
-        const BT_LDS uint16_t* p0 = (const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row1 * kRowBytes +
-                                                            ((c ^ swz(row1, kSlots)) * 16) + off);
-        vop[dt] = lds_read_tr4(p0);
-      }
-#pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] = mfma16k16(vop[dt], pop, oacc[dt]);
+    for (int dt = 0; dt < kDTiles; ++dt) {
+      const int c = dt * 2 + ((i16 & 3) >> 1);
+      vop[dt] = lds_read_tr4((const BT_LDS uint16_t*)((BT_LDS unsigned char*)vtile + row1 * kRowBytes +
+                                                      ((c ^ swz(row1, kSlots)) * 16) + (i16 & 1) * 8));
     }
-  };
-
-  // ---- tile loop: wave w takes local tiles w, w+WAVES, ... --------------------
-  if constexpr (PIPE == 1) {
-    for (int it = 0; it < my_tiles; ++it)
-      compute(tfirst + it * tstride, it + 1 < my_tiles, kr[0], vr[0]);
-  } else {
-    // Buffer b holds local tiles b, b + PIPE, ...; unrolled so every buffer
-    // index is a constant.
-    for (int it = 0; it < my_tiles; it += PIPE) {
 #pragma unroll
-      for (int b = 0; b < PIPE; ++b) {
-        if (it + b < my_tiles) {
-          const int t = tfirst + (it + b) * tstride;
-          compute(t, false, kr[b], vr[b]);
-          if (it + b + PIPE < my_tiles) {
-            load_k(t + PIPE * tstride, kr[b]);
-            load_v(t + PIPE * tstride, vr[b]);
-          }
-        }
-      }
-    }
+    for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] = mfma16k16(vop[dt], pop, oacc[dt]);
   }
 
   // ---- wave epilogue: full row sums, hi + lo merge ---------------------------
@@ -468,20 +394,19 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
   }
 
   // ---- cross-wave merge through LDS ----------------------------------------
-  float* mo = mlds;                                         // [wave][GMAX][kMoStride]
-  float* mm = mo + WAVES * GMAX * kMoStride;                // [wave][GMAX]
-  float* ml = mm + WAVES * GMAX;                            // [wave][GMAX]
-  // After the mirror sum, the hi lane (col = h) and the lo lane (col =
+  // After the mirror sum the hi lane (col = h) and the lo lane (col =
   // 2*GMAX-1-h) hold the same head-h sums: the hi lane stores the even
   // d-tiles and the lo lane the odd ones, so each store instruction carries
   // twice the lanes and a wave issues kDTiles/2 of them.
-  if (col_head >= 0 && col_head < G) {
+  float* mm = mstat;                // [wave][GMAX]
+  float* ml = mstat + W * GMAX;     // [wave][GMAX]
+  if (col_head >= 0) {
     const int par = col_lo ? 1 : 0;
-    float* dst = mo + (wave * GMAX + col_head) * kMoStride + par * 16 + kg * 4;
+    float* dst = mlds + (wave * GMAX + col_head) * kMoStride + par * 16 + kg * 4;
 #pragma unroll
     for (int q = 0; q < kDTiles / 2; ++q) {
-      const floatx4 a = oacc[2 * q], b = oacc[2 * q + 1];
-      const float4 v4 = {par ? b[0] : a[0], par ? b[1] : a[1], par ? b[2] : a[2], par ? b[3] : a[3]};
+      const floatx4 a = oacc[2 * q], c = oacc[2 * q + 1];
+      const float4 v4 = {par ? c[0] : a[0], par ? c[1] : a[1], par ? c[2] : a[2], par ? c[3] : a[3]};
       *reinterpret_cast<float4*>(dst + q * 32) = v4;
     }
     if (kg == 0 && !col_lo) {
@@ -497,16 +422,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gqa_decode_split_kernel(DecodeS
     const int d = (item % (D / 4)) * 4;
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, mm[w * GMAX + h]);
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, mm[w * GMAX + h]);
     float lsum = 0.f;
     float4 acc = {0.f, 0.f, 0.f, 0.f};
     // Branch-free, so all LDS reads are in flight together.  A wave without
     // valid tokens has l = 0, m = -inf and a zero partial: its weight is 0.
-    float4 ow[WAVES];
+    float4 ow[W];
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) ow[w] = *reinterpret_cast<const float4*>(mo + (w * GMAX + h) * kMoStride + d);
+    for (int w = 0; w < W; ++w) ow[w] = *reinterpret_cast<const float4*>(mlds + (w * GMAX + h) * kMoStride + d);
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float lw = ml[w * GMAX + h];
       const float sc = lw > 0.f ? fast_exp2(mm[w * GMAX + h] - mx) : 0.f;
       lsum += lw * sc;
@@ -545,6 +470,8 @@ __device__ __forceinline__ float wave_max(float x) {
 // 64-column chunk with LDS reductions.
 template <int D, bool RAGGED, int GROUPS>
 __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p) {
+  static_assert(GROUPS >= 1 && GROUPS <= 64 && (GROUPS & (GROUPS - 1)) == 0,
+                "split groups are a power of two that divides the 64 lanes");
   constexpr int kCols = 64 / GROUPS;   // float4 columns per wave
   constexpr int kPre = 128 / GROUPS;   // splits per lane fetched up front (GROUPS x kPre = 128)
   const int h = blockIdx.x;
@@ -628,20 +555,11 @@ __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p)
   }
 }
 
-// Production configuration of the split kernel.
-#ifndef BT_DECODE_WAVES
-#define BT_DECODE_WAVES 8
-#endif
-#ifndef BT_DECODE_PIPE
-#define BT_DECODE_PIPE 1
-#endif
-
 template <int GMAX, int D, int MODE, bool QBF16>
 static hipError_t launch_split_t(const DecodeSplitParams& p, int grid_x, int batch, hipStream_t stream) {
   dim3 grid(grid_x, p.kv_heads, batch);
-  hipLaunchKernelGGL(
-      (gqa_decode_split_kernel<GMAX, D, BT_DECODE_WAVES, BT_DECODE_TILE, BT_DECODE_PIPE, MODE, QBF16>),
-      grid, dim3(BT_DECODE_WAVES * 64), 0, stream, p);
+  hipLaunchKernelGGL((gqa_decode_split_kernel<GMAX, D, kDecodeWaves, MODE, QBF16>), grid, dim3(kDecodeWaves * 64), 0,
+                     stream, p);
   return hipGetLastError();
 }
 
