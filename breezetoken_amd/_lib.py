@@ -18,6 +18,7 @@ BT_ENOTSUP = -95
 BT_ENOSPC = -28
 BT_DTYPE_F32 = 0
 BT_DTYPE_BF16 = 1
+BT_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 _c_i32 = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -44,6 +45,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_vp, _c_i32, _c_i64, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32,
          _c_i32, _c_i32, _c_i32, _c_f32, _vp, _c_i64, _vp, _c_i32, _c_i64, _vp],
+    ),
+    "bt_gqa_decode_noalloc": (
+        ctypes.c_int,
+        [_vp, _c_i32, _c_i64, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32,
+         _c_i32, _c_i32, _c_i32, _c_f32, _vp, _c_i32, _c_i64, _vp],
     ),
     "bt_ragged_plan": (
         _c_i32,

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "../../include/breezetoken_amd.h"
@@ -226,6 +227,67 @@ int bt_gqa_decode(const void* q, int32_t q_dtype, int64_t q_stride_seq, const vo
   if (rc) return rc;
   return bt_gqa_decode_combine(lse, part, batch, heads, head_dim, num_split, nullptr, nullptr,
                                total, out, out_dtype, out_stride_seq, stream);
+}
+
+}  // extern "C"
+
+// Split workspace of bt_gqa_decode_noalloc: one copy per GPU, held from the
+// library's load on that GPU until the process ends.  Host code never names it
+// as a device address: it uses the pointer hipGetSymbolAddress returns for the
+// current device.
+static __device__ __align__(256) unsigned char scratch[BT_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return BT_ENOTSUP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (ptr == nullptr) return (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return BT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bt_gqa_decode_noalloc(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
+                          const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                          const int64_t* seq_offset, const int32_t* pos, const int32_t* seq_len,
+                          int32_t seqlen, int32_t batch, int32_t heads, int32_t kv_heads,
+                          int32_t head_dim, int32_t num_split, float scale, void* out,
+                          int32_t out_dtype, int64_t out_stride_seq, void* stream) {
+  int rc = check_decode_common(q, q_dtype, q_stride_seq, k, v, kv_stride_tok, kv_stride_head,
+                               batch, heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (num_split < 1) return BT_EINVAL;
+  if (num_split > bt::kMaxSplitsPerSeq || (int64_t)batch * num_split > INT32_MAX / 2) return BT_ENOTSUP;
+  if (bt_decode_workspace_bytes(heads, head_dim, batch * num_split) > (int64_t)BT_NOALLOC_SCRATCH_BYTES)
+    return BT_ENOSPC;
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc) return rc;
+  // Every split writes its lse (-inf when it has no tokens) before the combine
+  // reads it, and the combine reads only the partials of splits with tokens,
+  // so nothing left in the scratch by an earlier call is ever used.
+  return bt_gqa_decode(q, q_dtype, q_stride_seq, k, v, kv_stride_tok, kv_stride_head, seq_offset, pos,
+                       seq_len, seqlen, batch, heads, kv_heads, head_dim, num_split, scale, ws,
+                       (int64_t)BT_NOALLOC_SCRATCH_BYTES, out, out_dtype, out_stride_seq, stream);
 }
 
 int32_t bt_ragged_plan(const int32_t* lens, int32_t batch, int32_t target_groups, int32_t* work,

@@ -97,6 +97,28 @@ int bt_gqa_decode(const void* q, int32_t q_dtype, int64_t q_stride_seq, const vo
                   int64_t workspace_bytes, void* out, int32_t out_dtype,
                   int64_t out_stride_seq, void* stream);
 
+/* Bytes of the library's own decode scratch (see bt_gqa_decode_noalloc). */
+#define BT_NOALLOC_SCRATCH_BYTES (8 << 20)
+
+/* bt_gqa_decode without a caller workspace, for callers that cannot allocate
+ * (code under hipGraph capture that must not call hipMalloc, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in the reference,
+ * whose launch wrappers allocate Lse/Part per call (backends.py:531-533,
+ * 554-556).  The split workspace is a file-scope device array of
+ * BT_NOALLOC_SCRATCH_BYTES bytes, one per GPU, held from the library's load on
+ * that GPU until the process ends; nothing is allocated per call.  A shape whose
+ * bt_decode_workspace_bytes(heads, head_dim, batch*num_split) exceeds it returns
+ * BT_ENOSPC without launching (H = 8, D = 256 fits up to 1,019 splits; the
+ * configuration-2 grid uses 128).  All calls on one GPU share the array: calls
+ * that overlap on one GPU (two streams, two threads) race and must be
+ * serialised by the caller.  Arguments and results are those of bt_gqa_decode. */
+int bt_gqa_decode_noalloc(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
+                          const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                          const int64_t* seq_offset, const int32_t* pos, const int32_t* seq_len,
+                          int32_t seqlen, int32_t batch, int32_t heads, int32_t kv_heads,
+                          int32_t head_dim, int32_t num_split, float scale, void* out,
+                          int32_t out_dtype, int64_t out_stride_seq, void* stream);
+
 /* Host-side planner for ragged batches (no device access): given host lengths
  * lens[batch], choose per-sequence split counts ns_b = ceil(len_b / T) (at
  * least 1, at most ceil(len_b / 32)) for the smallest token cap T whose total
