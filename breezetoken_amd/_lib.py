@@ -64,7 +64,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "bt_prefill_split_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "bt_gqa_prefill": (
         ctypes.c_int,
-        [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+        [_vp, _c_i32, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
          _c_f32, _vp, _c_i64, _vp, _c_i32, _c_i64, _c_i64, _vp],
     ),
     "bt_rms_norm_rope": (

@@ -322,8 +322,9 @@ class HipBackend:
         out_dtype: torch.dtype = torch.float32, q_offset: int = 0, split_keys: bool = True,
     ) -> torch.Tensor:
         """Causal GQA prefill: q (S, H, D) are the new tokens at positions
-        q_offset .. q_offset + S - 1, k/v (q_offset + S, Hkv, D) the cache including
-        them (any token/head strides), all bf16 -> (S, H, D); row i attends keys
+        q_offset .. q_offset + S - 1 (f32, as the reference computes it, or bf16),
+        k/v (q_offset + S, Hkv, D) the bf16 cache including them (any token/head
+        strides) -> (S, H, D); row i attends keys
         0 .. q_offset + i.  q_offset = 0 is the SDPA call of prefill.py:56-68, a
         positive one the banded-mask chunked prefill of qwen36_moe.py:394-428.
         ``split_keys=False`` hands the library only the V^T workspace, which keeps
@@ -335,8 +336,8 @@ class HipBackend:
         q_offset = int(q_offset)
         if q_offset < 0 or k.shape[0] != q_offset + steps or k.shape[2] != dim or heads % groups:
             raise RuntimeError("prefill q/k/v shapes do not match (k/v need q_offset + S rows)")
-        if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
-            raise RuntimeError("the MFMA prefill serves bf16 q/k/v")
+        if q.dtype not in (torch.float32, torch.bfloat16) or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+            raise RuntimeError("the MFMA prefill serves f32 or bf16 q and bf16 k/v")
         if dim not in SERVED_PREFILL_HEAD_DIMS or heads // groups > MAX_GROUP:
             raise RuntimeError(f"prefill shape H={heads} Hkv={groups} D={dim} is not served")
         for t in (q, k, v):
@@ -350,7 +351,7 @@ class HipBackend:
         if not split_keys:
             ws_len = int(self._lib.bt_prefill_workspace_bytes(q_offset + steps, groups, dim))
         rc = self._lib.bt_gqa_prefill(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1),
+            q.data_ptr(), _dtype_code(q.dtype), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1),
             k.stride(0), k.stride(1), steps, q_offset, heads, groups, dim, float(scale),
             ws.data_ptr(), ws_len, out.data_ptr(), _dtype_code(out_dtype),
             out.stride(0), out.stride(1),

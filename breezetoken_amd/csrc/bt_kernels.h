@@ -72,6 +72,8 @@ struct PrefillParams {
   int out_bf16;
   int64_t out_stride_tok, out_stride_head;
   uint16_t* vt;        // workspace: fp16 V^T image, prefill_vt_bytes() bytes
+  int32_t* vexp;       // workspace: per (kv head, 64-key block) power-of-two scale of the image
+  int32_t q_f32;       // 1: q is f32 (split into bf16 high and low parts), 0: bf16
   // Split-key mode of the two-waves-per-SIMD kernel (kb_chunk > 0): work-group
   // (query block, kv head, chunk c) covers key blocks [c*kb_chunk, +kb_chunk);
   // a query block with more than one chunk writes one normalised partial and
@@ -211,6 +213,11 @@ hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stream);
 // Two-waves-per-SIMD prefill (gqa_prefill8.hip) for group sizes 1, 2, 4, 8.
 bool prefill8_serves(int group, int head_dim);
+// Pair kernel (gqa_prefill_pair.hip): two query blocks per work-group, 32
+// query columns per wave (16 with f32 q); group sizes 1, 2, 4, 8.
+bool prefill_pair_serves(int group, int head_dim, bool q_f32);
+int prefill_pair_grid(int seqlen, int group, int kv_heads, bool q_f32);
+hipError_t launch_prefill_pair(const PrefillParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_row_norm_rope(const RowPrepParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_attn_prep(const RowPrepParams& p, int head_dim, hipStream_t stream);

@@ -91,13 +91,32 @@ int device_cus() {
   return n;
 }
 
+// Prefill workspace: the fp16 V^T image, then (256-byte aligned) one int32
+// scale exponent per kv head and 64-key block.
+int64_t prefill_vexp_offset(int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
+  return align256((int64_t)bt::prefill_vt_bytes(kv_len, kv_heads, head_dim));
+}
+int64_t prefill_base_bytes(int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
+  const int64_t nblk = ((int64_t)kv_len + bt::kPrefillKeyBlock - 1) / bt::kPrefillKeyBlock;
+  return prefill_vexp_offset(kv_len, kv_heads, head_dim) + align256(nblk * kv_heads * 4);
+}
+
+// Long prompts whose pair grid fills the device run the pair kernel (it needs
+// no split-key partials); f32 q always does.
+bool prefill_uses_pair(int32_t seqlen, int32_t heads, int32_t kv_heads, int32_t head_dim, bool q_f32) {
+  const int group = heads / kv_heads;
+  if (!bt::prefill_pair_serves(group, head_dim, q_f32)) return false;
+  return q_f32 || bt::prefill_pair_grid(seqlen, group, kv_heads, false) >= device_cus();
+}
+
 // The split-key plan bt_gqa_prefill uses for this shape on the current device
 // (kb_chunk 0: none), and where its partials start in the workspace.
 bt::PrefillSplitPlan prefill_plan(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
                                   int32_t head_dim, int64_t* part_offset) {
-  *part_offset = align256((int64_t)bt::prefill_vt_bytes(q_offset + seqlen, kv_heads, head_dim));
+  *part_offset = align256(prefill_base_bytes(q_offset + seqlen, kv_heads, head_dim));
   const int group = heads / kv_heads;
   if (!bt::prefill8_serves(group, head_dim)) return bt::PrefillSplitPlan{};
+  if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim, false)) return bt::PrefillSplitPlan{};
   return bt::prefill8_split_plan(seqlen, q_offset, group, kv_heads, head_dim, device_cus());
 }
 
@@ -388,20 +407,20 @@ int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, c
 
 int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
   if (kv_len < 1 || kv_heads < 1 || head_dim < 1) return 0;
-  return (int64_t)bt::prefill_vt_bytes(kv_len, kv_heads, head_dim);
+  return prefill_base_bytes(kv_len, kv_heads, head_dim);
 }
 
 int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
                                          int32_t head_dim) {
   if (seqlen < 1 || q_offset < 0 || heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 1) return 0;
   if ((int64_t)q_offset + seqlen > INT32_MAX) return 0;
-  const int64_t vt = (int64_t)bt::prefill_vt_bytes(q_offset + seqlen, kv_heads, head_dim);
+  const int64_t vt = prefill_base_bytes(q_offset + seqlen, kv_heads, head_dim);
   int64_t part_offset = 0;
   const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
   return plan.kb_chunk > 0 ? part_offset + (int64_t)plan.part_bytes : vt;
 }
 
-int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
+int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,
                    int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
                    int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
                    int32_t head_dim, float scale, void* workspace, int64_t workspace_bytes,
@@ -411,6 +430,7 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   if (seqlen < 1 || q_offset < 0 || heads < 1 || kv_heads < 1 || heads % kv_heads) return BT_EINVAL;
   if ((int64_t)q_offset + seqlen > INT32_MAX) return BT_EINVAL;
   if (out_dtype != BT_DTYPE_F32 && out_dtype != BT_DTYPE_BF16) return BT_EINVAL;
+  if (q_dtype != BT_DTYPE_F32 && q_dtype != BT_DTYPE_BF16) return BT_EINVAL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return BT_EINVAL;
   if (q_stride_tok <= 0 || q_stride_head <= 0 || kv_stride_tok <= 0 || kv_stride_head < 0 ||
       out_stride_tok <= 0 || out_stride_head <= 0)
@@ -428,6 +448,8 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   if ((nblk + 1) * bt::kPrefillKeyBlock * kv_stride_tok * 2 > (int64_t)UINT32_MAX ||
       nblk * bt::kPrefillKeyBlock * head_dim * 2 > (int64_t)UINT32_MAX)
     return BT_ENOTSUP;
+  const bool q_f32 = q_dtype == BT_DTYPE_F32;
+  if (q_f32 && !bt::prefill_pair_serves(heads / kv_heads, head_dim, true)) return BT_ENOTSUP;
   if (workspace_bytes < bt_prefill_workspace_bytes(kv_len, kv_heads, head_dim)) return BT_ENOSPC;
   bt::PrefillParams p{};
   p.q = static_cast<const uint16_t*>(q);
@@ -448,6 +470,10 @@ int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride
   p.out_stride_tok = out_stride_tok;
   p.out_stride_head = out_stride_head;
   p.vt = static_cast<uint16_t*>(workspace);
+  p.vexp = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + prefill_vexp_offset(kv_len, kv_heads, head_dim));
+  p.q_f32 = q_f32 ? 1 : 0;
+  if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim, q_f32))
+    return hip_rc(bt::launch_prefill_pair(p, head_dim, (hipStream_t)stream));
   // Group sizes 1, 2, 4, 8 at D = 128 / 256 run two waves per SIMD; other
   // shapes take the one-wave-per-SIMD kernel.  Each writes its own fp16 V^T
   // image (laid out for its MFMA shape) into the same workspace size.  When

@@ -1,0 +1,662 @@
+// Causal GQA prefill for long prompts on CDNA4 MFMA: two query blocks per
+// work-group, 32 query columns per wave.
+//
+// Same contract as gqa_prefill8.hip (the causal SDPA of prefill.py:56-68 and
+// the banded chunked prefill of qwen36_moe.py:394-428: query row i at absolute
+// position q_offset + i attends keys 0 .. q_offset + i).  The work
+// decomposition is built for the long-prompt regime, where the kernel is
+// bound by LDS operand traffic per MFMA and by the causal triangle's uneven
+// work:
+//  * a wave holds 32 query columns (two 16-column q-tiles, Q^T in registers),
+//    so every K or V^T fragment it reads from LDS feeds two MFMAs -- half the
+//    LDS bytes per FLOP of one q-tile per wave.  O^T (D x 32 f32) is 128
+//    registers, Q^T 64; two waves still fit each SIMD;
+//  * 4 waves form a group that shares one K tile and one V^T tile of 32 keys
+//    per step (all heads of a GQA group read the same K/V);
+//  * a work-group holds two groups, A and B, and the query blocks j and
+//    N-1-j of one kv head: together they need N+1 steps whatever j is, so
+//    every work-group does the same work.  A runs block j, then the first
+//    keys of block N-1-j; B runs the remaining keys of block N-1-j; both take
+//    ceil((N+1)/2) steps in lockstep (one barrier per step), and the two
+//    halves of block N-1-j are merged through LDS at the end;
+//  * with f32 q (the reference keeps q in f32, prefill.py:49-68) a wave holds
+//    16 query columns and multiplies each K fragment with the bf16 high and
+//    low parts of q into the same accumulator: Q.K^T keeps ~16 mantissa bits;
+//  * P and V^T enter the P.V product as fp16 (P <= 2^8 from the lazily
+//    rescaled softmax); each 64-key block of V is stored scaled by its own
+//    power of two (prefill_vts_kernel), which the softmax folds into P, so V
+//    of any bf16 magnitude keeps fp16's 11 bits.
+#include "bt_common.h"
+#include "bt_kernels.h"
+
+namespace bt {
+
+namespace {
+
+typedef _Float16 halfx8_p __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_p __attribute__((ext_vector_type(2)));
+typedef float float2_p __attribute__((ext_vector_type(2)));
+
+constexpr int kUnit = 32;        // keys per step (one K tile and one V^T tile)
+constexpr int kGWaves = 4;       // waves per group
+constexpr float kLazyP = 8.0f;   // log2-domain slack before the reference max moves
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_p(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// HBM -> LDS copy of 16 bytes per lane (lane l's bytes land at lds + 16 * l);
+// offsets past the descriptor's range read as zero.
+__device__ __forceinline__ void dma16_p(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (BT_LDS void*)lds, 16, (int)voff, (int)soff, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma_bf16(const u32x4& a, const u32x4& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma_f16(const u32x4& a, const u32x4& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8_p, a), __builtin_bit_cast(halfx8_p, b), c,
+                                                0, 0, 0);
+}
+// Round to nearest even through a builtin (not asm), so the compiler sees the
+// VALU write and inserts the wait states an in-flight MFMA operand needs.
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_p){a, b}, half2_p));
+}
+// Scalar (constant-cache) read of a value another kernel wrote.
+__device__ __forceinline__ int sload(const int* p, int i) {
+  return ((const __attribute__((address_space(4))) int*)(p))[i];
+}
+
+}  // namespace
+
+// Pre-pass: V (kv_len, Hkv, D) bf16 -> fp16 V^T image for 16x16x32 MFMAs,
+// one power-of-two scale per 64-key block.  Block b of kv head g: e =
+// 4 * ceil((E - 14) / 4), E the binary exponent of the block's largest |v| (e
+// = -128 for a block of zeros); the image holds v * 2^-e, so its largest
+// magnitude is in [2^11, 2^15) and no value overflows fp16 or loses
+// precision to fp16's subnormal range.  e goes to vexp[g * nblk + b].  Layout:
+// block b of head g at vt + (g * nblk + b) * 64 * D; chunk c = kh*4 + q (kh:
+// 32-key half, q: lane group) holds at row d the 8 values of keys kh*32 + q*4 +
+// {0, 1, 2, 3, 16, 17, 18, 19} (16 bytes), the order in which a 16x16 result's
+// lane group q holds P.  Keys past kv_len are zero.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
+  constexpr int kDC = D / 8;                 // 16-byte column chunks per row
+  constexpr int kItems = 8 * kDC;            // (chunk, column chunk) items per block
+  static_assert(kItems <= 256, "one item per thread");
+  constexpr int kBlk = kPrefillKeyBlock;
+  const int blk = blockIdx.x, g = blockIdx.y;
+  const int nblk = gridDim.x;
+  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+  const __amdgpu_buffer_rsrc_t vrs =
+      rsrc_p(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)(p.q_offset + p.seqlen) * row_bytes);
+  uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kBlk * D;
+  constexpr int kUnits = kBlk * D * 2 / 16;
+  __shared__ __attribute__((aligned(16))) u32x4 stage[kUnits];
+  __shared__ uint32_t wmax[4];
+  const int item = threadIdx.x;
+  const int c = item / kDC, dc = item % kDC;
+  u32x4 rows[8];
+  uint32_t mx = 0;  // largest |v| as bf16 bits (monotonic for finite values)
+  if (item < kItems) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = blk * kBlk + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16;
+      rows[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((uint32_t)key * row_bytes + (uint32_t)dc * 16), 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = max(mx, max(rows[j][i] & 0x7fffu, (rows[j][i] >> 16) & 0x7fffu));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  int e = -128;
+  if (mx != 0) {
+    const int ebits = (int)(mx >> 7);                 // biased exponent (0: subnormal)
+    const int E = (ebits == 0 ? 1 : ebits) - 127;
+    e = -4 * ((14 - E) / 4);                          // 4 * ceil((E - 14) / 4) for E <= 14
+    if (E > 14) e = 4 * ((E - 14 + 3) / 4);
+  }
+  if (threadIdx.x == 0) p.vexp[g * nblk + blk] = e;
+  if (item < kItems) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // output row d = dc*8 + i
+      u32x4 o;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t w0 = rows[2 * m][i >> 1], w1 = rows[2 * m + 1][i >> 1];
+        const float f0 = __uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16));
+        const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
+        o[m] = pack_h2(__builtin_ldexpf(f0, -e), __builtin_ldexpf(f1, -e));
+      }
+      const int x = c * D + dc * 8 + i;
+      stage[x ^ ((x >> 3) & 7)] = o;
+    }
+  }
+  __syncthreads();
+  u32x4* dst = reinterpret_cast<u32x4*>(img);
+  for (int x = threadIdx.x; x < kUnits; x += 256) dst[x] = stage[x ^ ((x >> 3) & 7)];
+}
+
+namespace {
+
+// Shapes of the pair kernel's query blocks: a group covers 4 * NQT q-tiles of
+// 16 query positions each, for HG = min(G, 4 * NQT) heads of the kv group and
+// P = 16 * 4 * NQT / HG consecutive positions; G / HG head subgroups share a
+// kv head.
+struct PairShape {
+  int nqt, hg, pos, nsub;
+};
+__host__ __device__ inline PairShape pair_shape(int group, bool qf32) {
+  PairShape s;
+  s.nqt = qf32 ? 1 : 2;
+  s.hg = group < 4 * s.nqt ? group : 4 * s.nqt;
+  s.pos = 16 * 4 * s.nqt / s.hg;
+  s.nsub = group / s.hg;
+  return s;
+}
+
+// One group's share of a pair work-group.  GRP 0 (A) runs query block qa's
+// keys, then the first keys of qb; GRP 1 (B) the rest of qb.  K0/K1/V0/V1 are
+// this group's double-buffered tiles (distinct LDS objects, so the compiler
+// can tell a copy into one buffer from a read of another); xbuf(i) is tile
+// buffer i of the eight, reused for the final merge.
+template <bool B>
+struct Sel {
+  static constexpr bool value = B;
+};
+
+template <int D, bool QF32, int GRP, typename XB>
+__device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char* K0, unsigned char* K1,
+                                           unsigned char* V0, unsigned char* V1, XB xbuf, float* xs) {
+  constexpr int NQT = QF32 ? 1 : 2;
+  constexpr int kDSteps = D / 32;
+  constexpr int kDTiles = D / 16;
+  constexpr int kRowBytes = D * 2;
+  constexpr int kTile = kUnit * kRowBytes;           // 16 KiB at D = 256
+  constexpr int kCopies = kTile / 1024 / kGWaves;    // 1 KiB copies per wave per tile
+  static_assert(kCopies >= 1, "head_dim 128 or 256");
+  constexpr int kQParts = QF32 ? 2 : 1;              // hi and lo parts of q
+
+  const int lane = threadIdx.x & 63;
+  const int gw = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) & 3);
+  const int i16 = lane & 15;
+  const int g4 = lane >> 4;
+  const PairShape sh = pair_shape(p.group, QF32);
+  const int kvh = (int)blockIdx.y / sh.nsub;
+  const int sub = (int)blockIdx.y % sh.nsub;
+  const int S = p.seqlen;
+  const int P0 = p.q_offset;
+  const int nkeys = P0 + S;
+  const int nqb = (S + sh.pos - 1) / sh.pos;
+  const int qa = (int)blockIdx.x, qb = nqb - 1 - (int)blockIdx.x;
+  auto n_units = [&](int blk) { return (P0 + min(S, (blk + 1) * sh.pos) + kUnit - 1) / kUnit; };
+  const int na = qa != qb ? n_units(qa) : 0;
+  const int nb = n_units(qb);
+  // A runs block qa's na units, then the last xa units of block qb; B runs
+  // qb's first nb - xa units.  So both groups of every work-group read key
+  // unit s at step s for most of the kernel, and the work-groups on an XCD
+  // share each K/V tile through L2.  When na is odd A starts one step late,
+  // so its switch to block qb falls on an even step; the step count is even
+  // too.  Then the key loop is unrolled by two with a constant buffer per
+  // step and no branch between its copies.
+  const int lead = na & 1;
+  const int xa = max(0, (nb - na - lead) / 2);
+  const int steps_a = lead + na + xa;
+  const int steps_b = nb - xa;
+  const int n_steps = (max(steps_a, steps_b) + 1) & ~1;
+  const int my_steps = GRP == 0 ? steps_a : steps_b;
+  const int first = GRP == 0 ? lead : 0;          // this group's first working step
+  const int sw = lead + na;                        // A's first step on block qb (even)
+  // Unit of step s: (query block, key unit).
+  auto unit_blk = [&](int st) { return (GRP == 0 && st < sw) ? qa : qb; };
+  auto unit_key = [&](int st) { return GRP == 0 ? (st < sw ? st - lead : nb - xa + st - sw) : st; };
+
+  const int nblk64 = (nkeys + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
+  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+  const __amdgpu_buffer_rsrc_t krs = rsrc_p(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)nkeys * row_bytes);
+  const __amdgpu_buffer_rsrc_t vrs =
+      rsrc_p(p.vt + (size_t)kvh * nblk64 * kPrefillKeyBlock * D, (uint32_t)nblk64 * kPrefillKeyBlock * kRowBytes);
+  const int* vexp = p.vexp + kvh * nblk64;
+
+  // K copy j (1 KiB, rows 2j, 2j+1 at D = 256): lane l fetches, for slot s of
+  // row r, chunk s ^ (r & 15) -- the K tile lands row-major with an XOR
+  // swizzle, so the operand reads of 16 consecutive rows hit 16 bank groups.
+  constexpr int kSlots = D / 8;
+  constexpr int kRowsPerCopy = 1024 / kRowBytes;
+  auto k_voff = [&](int j) -> uint32_t {  // recomputed per copy: registers are scarce
+    const int r = (gw * kCopies + j) * kRowsPerCopy + lane / kSlots;
+    return (uint32_t)(lane / kSlots) * row_bytes + (uint32_t)((lane % kSlots) ^ (r & 15)) * 16;
+  };
+  auto copy_k = [&](unsigned char* kbuf, int u) {
+    const int key0 = unit_key(u) * kUnit;
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j)
+      dma16_p(krs, kbuf + (gw * kCopies + j) * 1024, k_voff(j),
+              (uint32_t)(key0 + (gw * kCopies + j) * kRowsPerCopy) * row_bytes);
+  };
+  auto copy_v = [&](unsigned char* vbuf, int u) {
+    const int key0 = unit_key(u) * kUnit;
+    // V^T: the 32-key half (key0 / 32) & 1 of 64-key block key0 / 64 is 16 KiB
+    // contiguous in the image.
+    const uint32_t vsrc = (uint32_t)(key0 / kPrefillKeyBlock) * (kPrefillKeyBlock * kRowBytes) +
+                          (uint32_t)((key0 / kUnit) & 1) * kTile;
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j) {
+      const int i = gw * kCopies + j;
+      dma16_p(vrs, vbuf + i * 1024, (uint32_t)lane * 16, vsrc + (uint32_t)i * 1024);
+    }
+  };
+
+  // ---- q-tiles of this wave -------------------------------------------------
+  // q-tile t of wave gw is group tile qt = gw * NQT + t: head (qt % HG) of the
+  // subgroup, positions [16 * (qt / HG), +16) of the query block.
+  int head[NQT], poff[NQT];
+#pragma unroll
+  for (int t = 0; t < NQT; ++t) {
+    const int qt = gw * NQT + t;
+    head[t] = kvh * p.group + sub * sh.hg + qt % sh.hg;
+    poff[t] = 16 * (qt / sh.hg);
+  }
+  // Q^T operand: lane (i16, g4) holds q[row][st*32 + g4*8 .. +8] of column i16.
+  // Rows past the prompt read the last row (their output is not stored).
+  u32x4 qop[NQT][kQParts][kDSteps];
+  auto load_q = [&](int blk) {
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      const int row = min(blk * sh.pos + poff[t] + i16, S - 1);
+      const int64_t off = (int64_t)row * p.q_stride_tok + (int64_t)head[t] * p.q_stride_head + g4 * 8;
+#pragma unroll
+      for (int st = 0; st < kDSteps; ++st) {
+        if constexpr (QF32) {
+          const float* qf = reinterpret_cast<const float*>(p.q) + off + st * 32;
+          const float4 a = *reinterpret_cast<const float4*>(qf);
+          const float4 b = *reinterpret_cast<const float4*>(qf + 4);
+          const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+          uint32_t hi[8], lo[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            hi[i] = f32_to_bf16_bits(v[i]);
+            lo[i] = f32_to_bf16_bits(v[i] - bf16_bits_to_f32(hi[i]));
+          }
+          qop[t][0][st] = u32x4{pack2(hi[0], hi[1]), pack2(hi[2], hi[3]), pack2(hi[4], hi[5]), pack2(hi[6], hi[7])};
+          qop[t][kQParts - 1][st] =
+              u32x4{pack2(lo[0], lo[1]), pack2(lo[2], lo[3]), pack2(lo[4], lo[5]), pack2(lo[6], lo[7])};
+        } else {
+          qop[t][0][st] = *reinterpret_cast<const u32x4*>(p.q + off + st * 32);
+        }
+      }
+    }
+  };
+
+  // ---- running state: per q-tile column (this lane's i16) -------------------
+  floatx4 oacc[NQT][kDTiles];
+  float m_ref[NQT], l_run[NQT];
+  int e_run = -128;   // scale exponent O is kept in: O_true = O * 2^e_run
+  auto reset = [&]() {
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+#pragma unroll
+      for (int i = 0; i < kDTiles; ++i) oacc[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+      m_ref[t] = -INFINITY;
+      l_run[t] = 0.f;
+    }
+    e_run = -128;
+  };
+  const float c_log2 = p.scale_log2;
+
+  // Normalise and store a finished block (rows past the prompt are skipped).
+  auto store = [&](int blk, const float (&lsum)[NQT]) {
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      const int row = blk * sh.pos + poff[t] + i16;
+      if (row >= S) continue;
+      const float inv = lsum[t] > 0.f ? __builtin_ldexpf(1.f / lsum[t], e_run) : 0.f;
+      const int64_t orow = (int64_t)row * p.out_stride_tok + (int64_t)head[t] * p.out_stride_head;
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
+        const int d = dt * 16 + g4 * 4;
+        const float o0 = oacc[t][dt][0] * inv, o1 = oacc[t][dt][1] * inv, o2 = oacc[t][dt][2] * inv,
+                    o3 = oacc[t][dt][3] * inv;
+        if (p.out_bf16) {
+          const u32x2 pk2 = {pack2(f32_to_bf16_bits(o0), f32_to_bf16_bits(o1)),
+                             pack2(f32_to_bf16_bits(o2), f32_to_bf16_bits(o3))};
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
+        } else {
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = float4{o0, o1, o2, o3};
+        }
+      }
+    }
+  };
+  auto row_sums = [&](float (&lsum)[NQT]) {
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      float l = l_run[t] + __shfl_xor(l_run[t], 16, 64);
+      lsum[t] = halves_sum(l);
+    }
+  };
+
+  // K operand of key tile kt, d-step st: chunk st*4 + g4 of row kt*16 + i16,
+  // in slot (st*4 + g4) ^ i16 = ((st ^ (i16 >> 2)) * 4) + ((g4 ^ i16) & 3).
+  uint32_t kaddr[4];
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4)
+    kaddr[s4] = (uint32_t)i16 * kRowBytes + (uint32_t)(((s4 ^ (i16 >> 2)) * 4 + ((g4 ^ i16) & 3)) * 16);
+  const uint32_t vaddr = (uint32_t)g4 * (D * 16) + (uint32_t)i16 * 16;  // V^T: chunk g4, row dt*16 + i16
+
+  // S^T = K.Q^T on the K tile kb, mask, online softmax: P^T of the step in pk.
+  u32x4 pk[NQT];
+  auto qk_sm = [&](const unsigned char* kb, int u) {
+    const int blk = unit_blk(u);
+    const int key0 = unit_key(u) * kUnit;
+    floatx4 sacc[2][NQT];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int t = 0; t < NQT; ++t) sacc[kt][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // K fragments are read one d-step ahead of their MFMAs (scheduling
+    // barriers keep the compiler from hoisting all of them: the registers are
+    // spoken for by O and Q).
+    auto kread = [&](int st, int kt) -> u32x4 {
+      return *reinterpret_cast<const u32x4*>(kb + kaddr[st & 3] + (st & 4) * 64 + kt * 16 * kRowBytes);
+    };
+    u32x4 ka0 = kread(0, 0), ka1 = kread(0, 1);
+#pragma unroll
+    for (int st = 0; st < kDSteps; ++st) {
+      u32x4 kn0 = ka0, kn1 = ka1;
+      if (st + 1 < kDSteps) {
+        kn0 = kread(st + 1, 0);
+        kn1 = kread(st + 1, 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NQT; ++t)
+#pragma unroll
+        for (int h = 0; h < kQParts; ++h) {
+          sacc[0][t] = mfma_bf16(ka0, qop[t][h][st], sacc[0][t]);
+          sacc[1][t] = mfma_bf16(ka1, qop[t][h][st], sacc[1][t]);
+        }
+      ka0 = kn0;
+      ka1 = kn1;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Causal mask: key key0 + kt*16 + g4*4 + r against this column's position.
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      const int qpos = P0 + blk * sh.pos + poff[t];  // first position of the q-tile
+      if (key0 + kUnit - 1 > qpos) {
+        const int mypos = qpos + i16;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (key0 + kt * 16 + g4 * 4 + r > mypos) sacc[kt][t][r] = -INFINITY;
+      }
+    }
+    // The V^T tile's scale: e of its 64-key block (wave-uniform).  P enters
+    // P.V as P' = P * 2^(eb - e_new) <= P (the shift rides in the exp2 bias);
+    // the row sum takes P, i.e. the sum of P' times 2^(e_new - eb).
+    const int eb = sload(vexp, key0 / kPrefillKeyBlock);
+    const int e_new = eb > e_run ? eb : e_run;
+    const float dshift = (float)(eb - e_new);
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      const floatx4& s0 = sacc[0][t];
+      const floatx4& s1 = sacc[1][t];
+      float tmax = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+      tmax = rows16_max(tmax);
+      tmax = halves_max(tmax) * c_log2;
+      const bool move = tmax > m_ref[t] + kLazyP;
+      const float m_new = move ? tmax : m_ref[t];
+      float alpha = move ? fast_exp2(m_ref[t] - m_new) : 1.f;  // 0 when m_ref is -inf
+      m_ref[t] = m_new;
+      const float bias = (m_new == -INFINITY ? 0.f : -m_new) + dshift;
+      float e[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        e[r] = fast_exp2(fmaf(s0[r], c_log2, bias));
+        e[4 + r] = fast_exp2(fmaf(s1[r], c_log2, bias));
+      }
+      float psum = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+      if (e_new != eb) psum = __builtin_ldexpf(psum, e_new - eb);  // wave-uniform, rare
+      l_run[t] = l_run[t] * alpha + psum;
+      if (e_new != e_run) alpha = __builtin_ldexpf(alpha, e_run - e_new);
+      // Key order of the V^T chunk g4: keys g4*4 + {0..3}, 16 + g4*4 + {0..3}.
+      pk[t] = u32x4{pack_h2(e[0], e[1]), pack_h2(e[2], e[3]), pack_h2(e[4], e[5]), pack_h2(e[6], e[7])};
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max or the V scale moved
+#pragma unroll
+        for (int i = 0; i < kDTiles; ++i) oacc[t][i] *= alpha;
+      }
+    }
+    e_run = e_new;
+  };
+  // O^T += V^T.P^T on the V^T tile vb.
+  auto pv = [&](const unsigned char* vb) {
+    auto vread = [&](int dt) -> u32x4 { return *reinterpret_cast<const u32x4*>(vb + vaddr + dt * 256); };
+    u32x4 va0 = vread(0), va1 = vread(1);
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; dt += 2) {
+#pragma unroll
+      for (int t = 0; t < NQT; ++t) oacc[t][dt] = mfma_f16(va0, pk[t], oacc[t][dt]);
+      if (dt + 2 < kDTiles) va0 = vread(dt + 2);
+#pragma unroll
+      for (int t = 0; t < NQT; ++t) oacc[t][dt + 1] = mfma_f16(va1, pk[t], oacc[t][dt + 1]);
+      if (dt + 3 < kDTiles) va1 = vread(dt + 3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Each wave waits for its own copies; a barrier publishes them (no
+  // __syncthreads: its fence would wait for every copy in flight).  vmcnt
+  // counts a wave's loads in issue order, so naming how many of the youngest
+  // may still be in flight waits for exactly the older ones.
+  auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+  constexpr int kWait1 = 0x0f70 | (kCopies & 0xf) | ((kCopies >> 4) << 14);            // vmcnt(kCopies)
+  constexpr int kWait2 = 0x0f70 | ((2 * kCopies) & 0xf) | (((2 * kCopies) >> 4) << 14);  // vmcnt(2 kCopies)
+  static_assert(2 * kCopies < 64, "vmcnt holds 6 bits");
+  // Wait until at most `younger` tiles' copies (kCopies each) are in flight:
+  // exactly the copies issued after the awaited tile, so none is under-waited.
+  auto wait_tiles = [&](int younger) {
+    if (younger >= 2) __builtin_amdgcn_s_waitcnt(kWait2);
+    else if (younger == 1) __builtin_amdgcn_s_waitcnt(kWait1);
+    else __builtin_amdgcn_s_waitcnt(0x0f70);
+  };
+
+  int cur_blk = unit_blk(first);
+  load_q(cur_blk);
+  reset();
+  if (first < my_steps) {
+    if (first & 1) { copy_k(K1, first); copy_v(V1, first); } else { copy_k(K0, first); copy_v(V0, first); }
+  }
+  auto working = [&](int st) { return st >= first && st < my_steps; };
+  // Each step has two barrier phases.  The two groups put their MFMA-heavy
+  // and VALU-heavy work in opposite phases, so the two waves that share a
+  // SIMD (one of each group) overlap one's softmax with the other's MFMAs:
+  //   A: | K_st ready  S = Q.K^T, softmax      | V_st ready  O += P.V       |
+  //   B: | V_st-1 ready  O += P_{st-1}.V_{st-1} | K_st ready  S = Q.K^T, softmax |
+  // Copies go out as soon as their buffer is free: A requests K and V^T of
+  // step st + 1 at the first barrier of st; B requests K of st + 1 at the first
+  // barrier and V^T of st + 1 at the second (after its P.V of st - 1).
+  auto step = [&](auto bufsel, int st) {
+    constexpr bool kOdd = decltype(bufsel)::value;
+    unsigned char* Kc = kOdd ? K1 : K0;   // this step's buffers
+    unsigned char* Vc = kOdd ? V1 : V0;
+    unsigned char* Kn = kOdd ? K0 : K1;   // the next step's (and the previous step's)
+    unsigned char* Vn = kOdd ? V0 : V1;
+    const bool w0 = working(st), w1 = working(st + 1);
+    // The wave running Q.K^T + softmax gets issue priority, so its MFMAs go
+    // first and its softmax overlaps the other wave's P.V.
+    if constexpr (GRP == 0) {
+      wait_tiles(1);  // K of st (its V^T was issued after it)
+      barrier();
+      if (w1) { copy_k(Kn, st + 1); copy_v(Vn, st + 1); }
+      __builtin_amdgcn_s_setprio(1);
+      if (w0) qk_sm(Kc, st);
+      __builtin_amdgcn_s_setprio(0);
+      wait_tiles(w1 ? 2 : 0);  // V^T of st (behind it: K and V^T of st + 1)
+      barrier();
+      if (w0) pv(Vc);
+    } else {
+      wait_tiles(w0 ? 2 : 0);  // V^T of st - 1 (behind it: K and V^T of st)
+      barrier();
+      if (w1) copy_k(Kn, st + 1);
+      if (working(st - 1)) pv(Vn);
+      wait_tiles((w0 ? 1 : 0) + (w1 ? 1 : 0));  // K of st (behind it: V^T of st, K of st + 1)
+      barrier();
+      if (w1) copy_v(Vn, st + 1);
+      __builtin_amdgcn_s_setprio(1);
+      if (w0) qk_sm(Kc, st);
+      __builtin_amdgcn_s_setprio(0);
+    }
+  };
+  auto run = [&](int s0, int s1) {  // s0 and s1 even
+    for (int st = s0; st < s1; st += 2) {
+      step(Sel<false>{}, st);
+      step(Sel<true>{}, st + 1);
+    }
+  };
+  if constexpr (GRP == 0) {
+    // Block qa, then (after storing it) the first keys of block qb.
+    const int s_switch = min(sw, n_steps);
+    run(0, s_switch);
+    if (na > 0 && s_switch < my_steps) {
+      float lsum[NQT];
+      row_sums(lsum);
+      store(cur_blk, lsum);
+      asm volatile("" ::: "memory");  // the next block's q loads stay behind these stores
+      cur_blk = qb;
+      load_q(qb);
+      reset();
+    }
+    run(s_switch, n_steps);
+  } else {
+    run(0, n_steps);
+  }
+
+  // B's P.V of its last step (both groups pass the barrier that publishes it).
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  barrier();
+  if constexpr (GRP == 1) {
+    if (working(n_steps - 1)) pv(V1);  // n_steps is even: its last step used buffer 1
+  }
+
+  // ---- merge the two halves of block qb --------------------------------------
+  float lsum[NQT];
+  row_sums(lsum);
+  barrier();  // every wave is done with every tile buffer
+  if constexpr (GRP == 0) {
+    if (cur_blk != qb) {  // A never reached qb: its qa result is final, its qb part empty
+      store(cur_blk, lsum);
+      reset();
+#pragma unroll
+      for (int t = 0; t < NQT; ++t) lsum[t] = 0.f;
+    }
+    // Hand A's qb partial (O, m, l, e) to the wave of B with the same q-tiles:
+    // q-tile t of wave gw goes through tile buffer gw * NQT + t.
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      float* dst = xbuf(gw * NQT + t);
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) *reinterpret_cast<floatx4*>(dst + (dt * 64 + lane) * 4) = oacc[t][dt];
+    }
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      xs[((gw * NQT + t) * 3 + 0) * 64 + lane] = m_ref[t];
+      xs[((gw * NQT + t) * 3 + 1) * 64 + lane] = lsum[t];
+    }
+    if (lane == 0) xs[kGWaves * NQT * 3 * 64 + gw] = __int_as_float(e_run);
+  }
+  barrier();
+  if constexpr (GRP == 1) {
+    const int ea = __float_as_int(xs[kGWaves * NQT * 3 * 64 + gw]);
+    const int e_m = ea > e_run ? ea : e_run;
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      const float ma = xs[((gw * NQT + t) * 3 + 0) * 64 + lane];
+      const float la = xs[((gw * NQT + t) * 3 + 1) * 64 + lane];
+      const float m = fmaxf(ma, m_ref[t]);
+      const float mu = m == -INFINITY ? 0.f : m;
+      const float wa = la > 0.f ? fast_exp2(ma - mu) : 0.f;
+      const float wb = lsum[t] > 0.f ? fast_exp2(m_ref[t] - mu) : 0.f;
+      const float sa = __builtin_ldexpf(wa, ea - e_m), sb = __builtin_ldexpf(wb, e_run - e_m);
+      const float* src = xbuf(gw * NQT + t);
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
+        const floatx4 oa = *reinterpret_cast<const floatx4*>(src + (dt * 64 + lane) * 4);
+        oacc[t][dt] = oacc[t][dt] * sb + oa * sa;
+        __builtin_amdgcn_sched_barrier(0);  // one tile of A's partial at a time
+      }
+      lsum[t] = la * wa + lsum[t] * wb;
+    }
+    e_run = e_m;
+    store(qb, lsum);
+  }
+}
+
+}  // namespace
+
+template <int D, bool QF32>
+__global__ __launch_bounds__(2 * kGWaves * 64, 1) void gqa_prefill_pair_kernel(PrefillParams p) {
+  constexpr int kTile = kUnit * D * 2;
+  constexpr int NQT = QF32 ? 1 : 2;
+  // Eight tile buffers (two per group per stage); after the key loop group A
+  // hands its partial to group B through the first ones.
+  __shared__ __attribute__((aligned(1024))) unsigned char kA0[kTile], kA1[kTile], vA0[kTile], vA1[kTile];
+  __shared__ __attribute__((aligned(1024))) unsigned char kB0[kTile], kB1[kTile], vB0[kTile], vB1[kTile];
+  __shared__ float xs[kGWaves * NQT * 3 * 64 + kGWaves];
+  static_assert(kGWaves * NQT <= 8 && (D / 16) * 64 * 16 <= kTile, "a q-tile's partial fits one tile buffer");
+  auto xbuf = [&](int i) -> float* {
+    unsigned char* b;
+    switch (i) {
+      case 0: b = kA0; break;
+      case 1: b = kA1; break;
+      case 2: b = vA0; break;
+      case 3: b = vA1; break;
+      case 4: b = kB0; break;
+      case 5: b = kB1; break;
+      case 6: b = vB0; break;
+      default: b = vB1; break;
+    }
+    return reinterpret_cast<float*>(b);
+  };
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (wave < kGWaves) pair_group<D, QF32, 0>(p, kA0, kA1, vA0, vA1, xbuf, xs);
+  else pair_group<D, QF32, 1>(p, kB0, kB1, vB0, vB1, xbuf, xs);
+}
+
+bool prefill_pair_serves(int group, int head_dim, bool q_f32) {
+  if (head_dim != 128 && head_dim != 256) return false;
+  if (group != 1 && group != 2 && group != 4 && group != 8) return false;
+  (void)q_f32;
+  return true;
+}
+
+int prefill_pair_grid(int seqlen, int group, int kv_heads, bool q_f32) {
+  const PairShape sh = pair_shape(group, q_f32);
+  const int nqb = (seqlen + sh.pos - 1) / sh.pos;
+  return ((nqb + 1) / 2) * kv_heads * sh.nsub;
+}
+
+hipError_t launch_prefill_pair(const PrefillParams& p, int head_dim, hipStream_t stream) {
+  const bool qf32 = p.q_f32 != 0;
+  const PairShape sh = pair_shape(p.group, qf32);
+  const int nqb = (p.seqlen + sh.pos - 1) / sh.pos;
+  const int nblk = (p.q_offset + p.seqlen + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
+  const dim3 grid((nqb + 1) / 2, p.kv_heads * sh.nsub), vt_grid(nblk, p.kv_heads);
+#define BT_PAIR_LAUNCH(DIM)                                                                            \
+  hipLaunchKernelGGL(prefill_vts_kernel<DIM>, vt_grid, dim3(256), 0, stream, p);                      \
+  if (qf32)                                                                                            \
+    hipLaunchKernelGGL((gqa_prefill_pair_kernel<DIM, true>), grid, dim3(2 * kGWaves * 64), 0, stream, p); \
+  else                                                                                                 \
+    hipLaunchKernelGGL((gqa_prefill_pair_kernel<DIM, false>), grid, dim3(2 * kGWaves * 64), 0, stream, p);
+  switch (head_dim) {
+    case 128: BT_PAIR_LAUNCH(128) break;
+    case 256: BT_PAIR_LAUNCH(256) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef BT_PAIR_LAUNCH
+  return hipGetLastError();
+}
+
+}  // namespace bt

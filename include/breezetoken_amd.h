@@ -147,10 +147,10 @@ int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, c
                          int64_t out_stride_seq, void* stream);
 
 /* Bytes of prefill workspace (the transposed fp16 V image the prefill builds
- * once per call) for kv_len = q_offset + seqlen keys; 0 for invalid
- * arguments.  Like bt_decode_workspace_bytes it replaces a per-call
- * allocation: the reference's SDPA call (prefill.py:60-68) allocates its
- * scratch internally. */
+ * once per call, with one power-of-two scale per 64-key block) for kv_len =
+ * q_offset + seqlen keys; 0 for invalid arguments.  Like
+ * bt_decode_workspace_bytes it replaces a per-call allocation: the
+ * reference's SDPA call (prefill.py:60-68) allocates its scratch internally. */
 int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t head_dim);
 
 /* Bytes of prefill workspace that also hold the split-key partials: with at
@@ -170,14 +170,16 @@ int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32
  * banded-mask chunked prefill of Qwen36MoE._attn_batch
  * (breezetoken/model/qwen36_moe.py:394-428; q_offset = pos0).  q (seqlen,
  * heads, D): the new tokens, at absolute positions q_offset .. q_offset +
- * seqlen - 1; k/v (q_offset + seqlen, kv_heads, D) bf16 with the given strides
+ * seqlen - 1, f32 (as the reference computes it, prefill.py:49-68; Q.K^T then
+ * uses its bf16 high and low parts; group sizes 1, 2, 4, 8) or bf16 (q_dtype);
+ * k/v (q_offset + seqlen, kv_heads, D) bf16 with the given strides
  * (token-major or head-major caches both fit): the cache including the new
  * tokens.  Query row i attends keys 0 .. q_offset + i.  out (seqlen, heads, D)
  * f32 or bf16.  `workspace` (16-byte aligned) must hold
  * bt_prefill_workspace_bytes(q_offset + seqlen, kv_heads, head_dim) bytes, and
  * bt_prefill_split_workspace_bytes(...) bytes for the split-key schedule; it is
  * scratch for the duration of the call on `stream`. */
-int bt_gqa_prefill(const void* q, const void* k, const void* v, int64_t q_stride_tok,
+int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,
                    int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
                    int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
                    int32_t head_dim, float scale, void* workspace, int64_t workspace_bytes,

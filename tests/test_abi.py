@@ -56,9 +56,10 @@ def test_workspace_bytes():
     assert lib.bt_decode_workspace_bytes(8, 256, 128) == 4096 + 8 * 128 * 256 * 4
     assert lib.bt_decode_workspace_bytes(8, 256, 1) == 256 + 8 * 256 * 4
     assert lib.bt_decode_workspace_bytes(0, 256, 1) == 0
-    # prefill: one fp16 V^T image per kv head, whole 64-key blocks
-    assert lib.bt_prefill_workspace_bytes(8192, 2, 256) == 2 * 8192 * 256 * 2
-    assert lib.bt_prefill_workspace_bytes(65, 1, 128) == 128 * 128 * 2
+    # prefill: one fp16 V^T image per kv head, whole 64-key blocks, then one
+    # int32 scale exponent per kv head and block (256-byte aligned)
+    assert lib.bt_prefill_workspace_bytes(8192, 2, 256) == 2 * 8192 * 256 * 2 + 1024
+    assert lib.bt_prefill_workspace_bytes(65, 1, 128) == 128 * 128 * 2 + 256
     assert lib.bt_prefill_workspace_bytes(0, 1, 128) == 0
     # the split-key size refuses the same malformed shapes (before any device query)
     assert lib.bt_prefill_split_workspace_bytes(0, 0, 8, 2, 256) == 0
@@ -171,21 +172,21 @@ def test_entry_points_refuse_bad_arguments_before_launching():
     assert rc == _lib.BT_ENOTSUP
     # prefill: unserved head dim, bad strides or offset, missing or short workspace
     big = 1 << 30
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 0, 8, 2, 64, 0.125, fake, big,
+    rc = lib.bt_gqa_prefill(fake, 1, fake, fake, 2048, 256, 512, 256, 16, 0, 8, 2, 64, 0.125, fake, big,
                             fake, 0, 2048, 256, None)
     assert rc == _lib.BT_ENOTSUP
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 0, 0, 8, 2, 256, 0.0625, fake, big,
+    rc = lib.bt_gqa_prefill(fake, 1, fake, fake, 2048, 256, 512, 256, 0, 0, 8, 2, 256, 0.0625, fake, big,
                             fake, 0, 2048, 256, None)
     assert rc == _lib.BT_EINVAL
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, -1, 8, 2, 256, 0.0625, fake, big,
+    rc = lib.bt_gqa_prefill(fake, 1, fake, fake, 2048, 256, 512, 256, 16, -1, 8, 2, 256, 0.0625, fake, big,
                             fake, 0, 2048, 256, None)
     assert rc == _lib.BT_EINVAL
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 0, 8, 2, 256, 0.0625, None, big,
+    rc = lib.bt_gqa_prefill(fake, 1, fake, fake, 2048, 256, 512, 256, 16, 0, 8, 2, 256, 0.0625, None, big,
                             fake, 0, 2048, 256, None)
     assert rc == _lib.BT_EINVAL
     # the V^T workspace covers q_offset + seqlen keys
     need = lib.bt_prefill_workspace_bytes(16 + 100, 2, 256)
-    rc = lib.bt_gqa_prefill(fake, fake, fake, 2048, 256, 512, 256, 16, 100, 8, 2, 256, 0.0625, fake,
+    rc = lib.bt_gqa_prefill(fake, 1, fake, fake, 2048, 256, 512, 256, 16, 100, 8, 2, 256, 0.0625, fake,
                             need - 1, fake, 0, 2048, 256, None)
     assert rc == _lib.BT_ENOSPC
 
@@ -260,21 +261,23 @@ def test_gemv_refuses_bad_arguments_and_sizes_its_workspace():
         (512, 0, 8, 4),
         (2048, 0, 8, 2),
         (1024, 0, 8, 4),
-        # a grid of a work-group per CU or more is not split
+        # a grid of a work-group per CU or more is not split (8192: the pair kernel)
         (4096, 0, 8, 0),
         (8192, 0, 8, 0),
     ],
 )
 def test_prefill_split_plan_sizes(steps, q_offset, heads, max_chunks):
     """The split-key plan on a 256-CU device (the count assumed without a GPU):
-    the workspace is the V^T image plus f32 partials and LSEs of
-    kv_heads x query blocks x max_chunks x 128 rows."""
+    the workspace is the V^T image and its block scales plus f32 partials and
+    LSEs of kv_heads x query blocks x max_chunks x 128 rows.  S = 8192 runs the
+    pair kernel, which needs no partials."""
     from breezetoken_amd import _lib
 
     lib = _lib.lib()
     kv, dim = 2, 256
     vt = lib.bt_prefill_workspace_bytes(q_offset + steps, kv, dim)
-    assert vt == kv * -(-(q_offset + steps) // 64) * 64 * dim * 2
+    nblk = -(-(q_offset + steps) // 64)
+    assert vt == kv * nblk * 64 * dim * 2 + -(-(kv * nblk * 4) // 256) * 256
     got = lib.bt_prefill_split_workspace_bytes(steps, q_offset, heads, kv, dim)
     if max_chunks == 0:
         assert got == vt

@@ -165,7 +165,8 @@ def _prefill_with_workspace(q, k, v, scale, q_offset, ws_bytes):
     out = torch.empty((steps, heads, dim), dtype=torch.float32, device="cuda")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
     rc = _lib.lib().bt_gqa_prefill(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+        q.data_ptr(), _lib.BT_DTYPE_BF16, k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1), k.stride(0),
+        k.stride(1),
         steps, q_offset, heads, k.shape[1], dim, float(scale), ws.data_ptr(), ws_bytes, out.data_ptr(),
         _lib.BT_DTYPE_F32, out.stride(0), out.stride(1),
         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
