@@ -38,6 +38,12 @@ typedef _Float16 half2_p __attribute__((ext_vector_type(2)));
 typedef float float2_p __attribute__((ext_vector_type(2)));
 
 constexpr int kUnit = 32;        // keys per step (one K tile and one V^T tile)
+// LDS fragment reads in flight ahead of their MFMAs: K two d-steps ahead in
+// S = K.Q^T, V^T four d-tiles ahead in O^T += V^T.P^T.  C4 at S = 8192, bf16
+// q, same run: lead 1/2 -> 325 us, 2/2 -> 314-320, 1/4 -> 312-314, 2/4 ->
+// 300-317, 3/4 and 2/8 -> 332-340 (the bf16 kernel then spills in the loop).
+constexpr int kKLead = 2;
+constexpr int kVLead = 4;
 constexpr int kGWaves = 4;       // waves per group
 constexpr float kLazyP = 8.0f;   // log2-domain slack before the reference max moves
 
@@ -356,29 +362,33 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int t = 0; t < NQT; ++t) sacc[kt][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    // K fragments are read one d-step ahead of their MFMAs (scheduling
+    // K fragments are read kKLead d-steps ahead of their MFMAs (scheduling
     // barriers keep the compiler from hoisting all of them: the registers are
     // spoken for by O and Q).
     auto kread = [&](int st, int kt) -> u32x4 {
       return *reinterpret_cast<const u32x4*>(kb + kaddr[st & 3] + (st & 4) * 64 + kt * 16 * kRowBytes);
     };
-    u32x4 ka0 = kread(0, 0), ka1 = kread(0, 1);
+    constexpr int KLA = kKLead;
+    u32x4 kf[KLA + 1][2];
+#pragma unroll
+    for (int i = 0; i < KLA; ++i) {
+      kf[i][0] = kread(i, 0);
+      kf[i][1] = kread(i, 1);
+    }
 #pragma unroll
     for (int st = 0; st < kDSteps; ++st) {
-      u32x4 kn0 = ka0, kn1 = ka1;
-      if (st + 1 < kDSteps) {
-        kn0 = kread(st + 1, 0);
-        kn1 = kread(st + 1, 1);
+      if (st + KLA < kDSteps) {
+        kf[(st + KLA) % (KLA + 1)][0] = kread(st + KLA, 0);
+        kf[(st + KLA) % (KLA + 1)][1] = kread(st + KLA, 1);
       }
+      const u32x4 a0 = kf[st % (KLA + 1)][0], a1 = kf[st % (KLA + 1)][1];
 #pragma unroll
       for (int t = 0; t < NQT; ++t)
 #pragma unroll
         for (int h = 0; h < kQParts; ++h) {
-          sacc[0][t] = mfma_bf16(ka0, qop[t][h][st], sacc[0][t]);
-          sacc[1][t] = mfma_bf16(ka1, qop[t][h][st], sacc[1][t]);
+          sacc[0][t] = mfma_bf16(a0, qop[t][h][st], sacc[0][t]);
+          sacc[1][t] = mfma_bf16(a1, qop[t][h][st], sacc[1][t]);
         }
-      ka0 = kn0;
-      ka1 = kn1;
       __builtin_amdgcn_sched_barrier(0);
     }
     // Causal mask: key key0 + kt*16 + g4*4 + r against this column's position.
@@ -434,16 +444,17 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // O^T += V^T.P^T on the V^T tile vb.
   auto pv = [&](const unsigned char* vb) {
     auto vread = [&](int dt) -> u32x4 { return *reinterpret_cast<const u32x4*>(vb + vaddr + dt * 256); };
-    u32x4 va0 = vread(0), va1 = vread(1);
+    constexpr int VLA = kVLead;
+    u32x4 vf[VLA];
 #pragma unroll
-    for (int dt = 0; dt < kDTiles; dt += 2) {
+    for (int i = 0; i < VLA; ++i) vf[i] = vread(i);
 #pragma unroll
-      for (int t = 0; t < NQT; ++t) oacc[t][dt] = mfma_f16(va0, pk[t], oacc[t][dt]);
-      if (dt + 2 < kDTiles) va0 = vread(dt + 2);
+    for (int dt = 0; dt < kDTiles; ++dt) {
+      const u32x4 a = vf[dt % VLA];
+      if (dt + VLA < kDTiles) vf[dt % VLA] = vread(dt + VLA);
 #pragma unroll
-      for (int t = 0; t < NQT; ++t) oacc[t][dt + 1] = mfma_f16(va1, pk[t], oacc[t][dt + 1]);
-      if (dt + 3 < kDTiles) va1 = vread(dt + 3);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int t = 0; t < NQT; ++t) oacc[t][dt] = mfma_f16(a, pk[t], oacc[t][dt]);
+      if (dt % 2 == 1) __builtin_amdgcn_sched_barrier(0);
     }
   };
 
