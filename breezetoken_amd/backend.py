@@ -62,6 +62,73 @@ def rope_tables(cap: int, rope_dim: int, theta: float, device: str | torch.devic
     return freqs.cos(), freqs.sin()
 
 
+def decode_unserved(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, device: torch.device | None = None) -> str | None:
+    """Why the decode kernels cannot take ``attention(q, k, v, scale)``, or None
+    when they can: q (H, D) f32/bf16, k/v equal (S >= 1, Hkv, D) bf16 with
+    unit d-stride and identical strides, D in SERVED_HEAD_DIMS, H / Hkv <= 8,
+    one sequence's KV extent below 4 GiB, every tensor on ``device`` (a GPU
+    device; None checks only that they share one GPU)."""
+    if q.ndim != 2 or k.ndim != 3 or v.ndim != 3:
+        return "attention expects q (H, D), k/v (S, Hkv, D)"
+    if v.shape != k.shape:
+        return "k/v must be (S, Hkv, D) with equal shapes"
+    heads, dim = q.shape
+    groups = k.shape[1]
+    if groups < 1 or k.shape[2] != dim or heads % groups:
+        return f"q heads {heads} / kv {tuple(k.shape)} do not form a GQA group"
+    if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        return "the MI355X path serves a bf16 KV cache only"
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        return "q must be f32 or bf16"
+    if dim not in SERVED_HEAD_DIMS or heads // groups > MAX_GROUP:
+        return f"shape H={heads} Hkv={groups} D={dim} is not served"
+    if k.shape[0] < 1:
+        return "attention needs at least one key"
+    if k.stride(2) != 1 or k.stride() != v.stride():
+        return "k/v need unit d-stride and identical strides"
+    if k.shape[0] * k.stride(0) * 2 >= 1 << 32:
+        return "one sequence's KV extent must stay below 4 GiB"
+    want = device if device is not None else q.device
+    if want.type != "cuda" or any(t.device != want for t in (q, k, v)):
+        return "q/k/v must live on the backend's GPU"
+    return None
+
+
+def prefill_unserved(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offset: int = 0,
+                     device: torch.device | None = None) -> str | None:
+    """Why ``attention_prefill(q, k, v, scale, q_offset=q_offset)`` cannot run
+    on the prefill kernels, or None when it can: q (S, H, D) f32/bf16, k/v
+    equal (q_offset + S, Hkv, D) bf16, unit d-stride, identical k/v strides,
+    D in SERVED_PREFILL_HEAD_DIMS, H / Hkv <= 8, all on one GPU."""
+    if q.ndim != 3 or k.ndim != 3 or v.shape != k.shape:
+        return "prefill expects q (S, H, D), k/v (q_offset + S, Hkv, D)"
+    steps, heads, dim = q.shape
+    groups = k.shape[1]
+    if q_offset < 0 or groups < 1 or k.shape[0] != q_offset + steps or k.shape[2] != dim or heads % groups:
+        return "prefill q/k/v shapes do not match (k/v need q_offset + S rows)"
+    if q.dtype not in (torch.float32, torch.bfloat16) or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        return "the MFMA prefill serves f32 or bf16 q and bf16 k/v"
+    if dim not in SERVED_PREFILL_HEAD_DIMS or heads // groups > MAX_GROUP:
+        return f"prefill shape H={heads} Hkv={groups} D={dim} is not served"
+    if any(t.stride(2) != 1 for t in (q, k, v)):
+        return "prefill needs unit d-stride"
+    if k.stride() != v.stride():
+        return "k and v need identical strides"
+    if any(st <= 0 or st % 8 for st in (q.stride(0), q.stride(1), k.stride(0))) or k.stride(1) < 0 or k.stride(1) % 8:
+        return "prefill needs token/head strides in positive multiples of 8 elements"
+    if any(t.data_ptr() % 16 for t in (q, k, v)):
+        return "prefill needs 16-byte aligned q/k/v"
+    if q.dtype == torch.float32 and heads // groups not in (1, 2, 4, 8):
+        return "f32 q is served for group sizes 1, 2, 4 and 8 (narrow q to bf16 for others)"
+    nblk = -(-k.shape[0] // 64)
+    if (nblk + 1) * 64 * k.stride(0) * 2 > 0xFFFFFFFF or nblk * 64 * dim * 2 > 0xFFFFFFFF:
+        return "one kv head's K rows and V^T image must stay below 4 GiB"
+    want = device if device is not None else q.device
+    if want.type != "cuda" or any(t.device != want for t in (q, k, v)):
+        return "q/k/v must live on the backend's GPU"
+    return None
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -146,6 +213,16 @@ class HipBackend:
         if k.shape[0] * k.stride(0) * 2 >= 1 << 32:
             raise RuntimeError("one sequence's KV extent must stay below 4 GiB")
         return groups
+
+    def serves_decode(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+        """True when ``attention(q, k, v, scale)`` runs on the decode kernels;
+        False where it would raise for the shape, dtype, layout or device."""
+        return decode_unserved(q, k, v, self._dev) is None
+
+    def serves_prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offset: int = 0) -> bool:
+        """True when ``attention_prefill(q, k, v, scale, q_offset=...)`` runs on
+        the prefill kernels."""
+        return prefill_unserved(q, k, v, int(q_offset), self._dev) is None
 
     # ----------------------------------------------------------- decode (eager)
     def attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> torch.Tensor:

@@ -98,4 +98,30 @@ __device__ __forceinline__ float halves_sum(float x) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
+// Scaled fp16 V^T images of the prefill kernels: 64-key block b of a kv head
+// holds v * 2^-e_b with e_b = 4 * ceil((E - 14) / 4), E the binary exponent of
+// the block's largest |v| (e_b in [-140, 116]), or kVExpZero for a block of
+// zeros.
+constexpr int kVExpZero = -1024;
+
+// Exponent e of the units the O accumulator is kept in (O_true = O * 2^e)
+// after a block with exponent eb: unchanged for a zero block and for a block
+// within 4 of it (P then carries the block's factor 2^(eb - e) <= 2^4 exactly
+// in fp16), else the block's own -- but at most 64 below the current one, so
+// the f32 accumulator cannot overflow; a block more than 2^64 below the
+// running scale enters with its P shifted down by the excess.
+__device__ __forceinline__ int vexp_next(int e_run, int eb) {
+  if (eb == kVExpZero) return e_run;
+  if (e_run == kVExpZero) return eb;
+  const int d = eb - e_run;
+  if (d >= -4 && d <= 4) return e_run;
+  return d < -64 ? e_run - 64 : eb;
+}
+// Scalar (constant-cache) read of a value an earlier kernel wrote.
+__device__ __forceinline__ int sload(const int* p, int i) {
+  return ((const __attribute__((address_space(4))) int*)(p))[i];
+}
+// Power-of-two factor of a block's P: P' = P * 2^shift enters P.V.
+__device__ __forceinline__ int vexp_shift(int e_new, int eb) { return eb == kVExpZero ? 0 : eb - e_new; }
+
 }  // namespace bt

@@ -179,8 +179,8 @@ inline size_t gemv_workspace_bytes(int K, int N) {
   return sk == 1 ? 0 : (size_t)sk * N * 4;
 }
 
-// Keys per block of the prefill key loop, and the size of the transposed fp16
-// V image the prefill builds in its workspace: per kv head and 64-key block,
+// Keys per block of the prefill key loop, and the size of the transposed,
+// block-scaled fp16 V image the prefill builds in its workspace: per kv head and 64-key block,
 // 8 chunks of 8 keys x head_dim rows x 16 bytes, for kv_len keys.
 constexpr int kPrefillKeyBlock = 64;
 inline size_t prefill_vt_bytes(int kv_len, int kv_heads, int head_dim) {
@@ -218,6 +218,11 @@ bool prefill8_serves(int group, int head_dim);
 bool prefill_pair_serves(int group, int head_dim, bool q_f32);
 int prefill_pair_grid(int seqlen, int group, int kv_heads, bool q_f32);
 hipError_t launch_prefill_pair(const PrefillParams& p, int head_dim, hipStream_t stream);
+// Scaled fp16 V^T image + per-block exponents (p.vt, p.vexp) in the key order
+// of the 16x16 (kVtOrder16) or 32x32 (kVtOrder32) MFMA result layout.
+constexpr int kVtOrder16 = 0;
+constexpr int kVtOrder32 = 1;
+hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, int order, hipStream_t stream);
 hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_row_norm_rope(const RowPrepParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_attn_prep(const RowPrepParams& p, int head_dim, hipStream_t stream);

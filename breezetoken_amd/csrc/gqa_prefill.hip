@@ -10,9 +10,10 @@
 // Qwen36MoE._attn_batch (breezetoken/model/qwen36_moe.py:394-428).
 //
 // Decomposition (MI355X-first):
-//  * a small pre-pass writes V once per kv head as a transposed fp16 image
-//    (V^T in 8-key chunks; exact for |v| <= 65504, larger values saturate), so
-//    the key loop needs neither a conversion nor a transposing LDS read;
+//  * a small pre-pass (gqa_prefill_vt.hip, key order kVtOrder32) writes V
+//    once per kv head as a transposed fp16 image scaled by a power of two per
+//    64-key block, so the key loop needs neither a conversion nor a
+//    transposing LDS read, and every finite bf16 V fits fp16;
 //  * one work-group (4 waves) per (block of query positions, kv head); wave w
 //    owns query head w of the GQA group (and, for G < 4, a different block of
 //    positions), so every K/V tile staged in LDS feeds all G heads;
@@ -77,11 +78,6 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* l
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (BT_LDS void*)lds, 16, (int)voff, (int)soff, 0, 0);
 }
 
-// Two floats -> packed fp16 pair, round toward zero (bf16 values convert exactly;
-// out-of-range magnitudes saturate to +-65504 instead of becoming inf).
-__device__ __forceinline__ uint32_t pack_f16_rtz(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
-}
 // Two floats -> packed fp16 pair, round to nearest even (one v_cvt_pk_f16_f32).
 // A builtin, not asm: the compiler must see this VALU write to insert the wait
 // states a VGPR needs after an in-flight MFMA has read it as an operand.
@@ -106,57 +102,6 @@ __device__ __forceinline__ void interleave() {
 }
 
 }  // namespace
-
-// ---------------------------------------------------------------------------
-// Pre-pass: V (S, Hkv, D) bf16 -> fp16 V^T image.  Key block b of kv head g is
-// stored at vt + (g * nblk + b) * 64 * D as 8 key chunks; chunk c = 2 * ks + h
-// holds, for every d, the values V[b*64 + key][d] of the 8 keys
-//     key = ks*16 + h*4 + {0, 1, 2, 3, 8, 9, 10, 11}
-// (16 bytes) at row d.  That is the key order in which lane l of the P^T
-// operand holds P: the 32x32 MFMA result puts key (j/4)*8 + (l/32)*4 + j%4 of
-// a 32-key half in register j, and each 16-key step takes 8 consecutive
-// registers.  Keys past the prompt are zero.  Each thread transposes 8 x 8
-// tiles (one chunk, dims dc*8..) in registers.
-template <int D>
-__global__ __launch_bounds__(256) void prefill_vt_kernel(PrefillParams p) {
-  constexpr int kDC = D / 8;
-  const int blk = blockIdx.x, g = blockIdx.y;
-  const int nblk = gridDim.x;
-  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-  const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)(p.q_offset + p.seqlen) * row_bytes);
-  uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kKB * D;
-  // The block's image is assembled in LDS and stored linearly (1 KiB per wave
-  // instruction) instead of as each thread's 128 contiguous bytes; 16-byte
-  // unit x sits in LDS slot x ^ ((x >> 3) & 7), conflict-free both ways.
-  constexpr int kUnits = kKB * D * 2 / 16;
-  __shared__ __attribute__((aligned(16))) u32x4 stage[kUnits];
-  for (int item = threadIdx.x; item < 8 * kDC; item += 256) {
-    const int c = item / kDC, dc = item % kDC;
-    u32x4 rows[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int key = blk * kKB + (c >> 1) * 16 + (c & 1) * 4 + (j & 3) + (j >> 2) * 8;
-      rows[j] = buf_load16(vrs, (uint32_t)key * row_bytes + (uint32_t)dc * 16, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {  // output row d = dc*8 + i
-      u32x4 o;
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const uint32_t w0 = rows[2 * m][i >> 1], w1 = rows[2 * m + 1][i >> 1];
-        const float f0 = __uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16));
-        const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
-        o[m] = pack_f16_rtz(f0, f1);
-      }
-      const int x = c * D + dc * 8 + i;
-      stage[x ^ ((x >> 3) & 7)] = o;
-    }
-  }
-  __syncthreads();
-  u32x4* dst = reinterpret_cast<u32x4*>(img);
-  for (int x = threadIdx.x; x < kUnits; x += 256) dst[x] = stage[x ^ ((x >> 3) & 7)];
-}
 
 // D: head dim (128 or 256).  Wave w of a work-group handles query head
 // (pass * 4 + w % GW) of the group and positions [q0 + (w / GW) * 32, +32),
@@ -212,6 +157,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
   const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)nkeys * row_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.vt + (size_t)kvh * nblk * kKB * D, (uint32_t)nblk * kImg);
+  const int* vexp = p.vexp + kvh * nblk;
   const uint32_t k_voff = (uint32_t)lane * row_bytes;
   const uint32_t v_voff = (uint32_t)lane * 16;
   auto copy_k = [&](auto b, int kb) {
@@ -273,6 +219,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       for (int j = 0; j < 16; ++j) oacc[i][j] = 0.f;
     float m_ref = -INFINITY;  // reference max (log2 domain) of this lane's column
     float l_run = 0.f;        // partial row sum over this lane's keys
+    int e_run = kVExpZero;    // V scale O is kept in: O_true = O * 2^e_run
+    int tail_shift = 0;       // P' = P * 2^tail_shift of the pending keys 32..63
     const int my_q = q0 + qcol;       // this lane's query row
     const int my_pos = P0 + my_q;     // its absolute position: keys 0..my_pos
     // P of a key block as fp16 pairs: pk0 holds keys 0..31 of the block, pk1
@@ -339,9 +287,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     };
     // Online softmax, first part: block max, lazy reference-max update, P of
     // keys 0..31 into out.  Returns the factor the accumulated O must be
-    // scaled by (1 unless the reference max moved).  Keys 32..63 follow in
-    // softmax_tail beside the next block's S = K.Q^T.
-    auto softmax_head = [&](floatx16(&sacc)[2], uint32_t(&out)[8]) -> float {
+    // scaled by (1 unless the reference max or the V scale moved).  Keys
+    // 32..63 follow in softmax_tail beside the next block's S = K.Q^T.  The
+    // V^T block's power-of-two scale enters P' = P * 2^shift through the exp2
+    // bias; the row sum takes P.
+    auto softmax_head = [&](int kb, floatx16(&sacc)[2], uint32_t(&out)[8]) -> float {
       float tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -353,12 +303,23 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       const float m_new = move ? tmax : m_ref;
       const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
       m_ref = m_new;
-      neg_m_tail = m_ref == -INFINITY ? 0.f : -m_ref;
-      l_run = l_run * alpha + exp_half(sacc[0], neg_m_tail, out);
+      const int eb = sload(vexp, kb);
+      const int e_new = vexp_next(e_run, eb);
+      tail_shift = vexp_shift(e_new, eb);
+      neg_m_tail = (m_ref == -INFINITY ? 0.f : -m_ref) + (float)tail_shift;
+      float psum = exp_half(sacc[0], neg_m_tail, out);
+      if (tail_shift != 0) psum = __builtin_ldexpf(psum, -tail_shift);  // wave-uniform, rare
+      l_run = l_run * alpha + psum;
       s_tail = sacc[1];
-      return alpha;
+      const float factor = e_new != e_run ? __builtin_ldexpf(alpha, e_run - e_new) : alpha;
+      e_run = e_new;
+      return factor;
     };
-    auto softmax_tail = [&] { l_run += exp_half(s_tail, neg_m_tail, pk1); };
+    auto softmax_tail = [&] {
+      float psum = exp_half(s_tail, neg_m_tail, pk1);
+      if (tail_shift != 0) psum = __builtin_ldexpf(psum, -tail_shift);
+      l_run += psum;
+    };
     auto rescale = [&](float alpha) {
       if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max moved by > 2^8
 #pragma unroll
@@ -389,7 +350,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       barrier();  // every wave is done reading K_0
       copy_k(Buf<0>{}, min(2, last));
       if (0 >= kb_diag) mask(0, sacc);
-      rescale(softmax_head(sacc, pk0));
+      rescale(softmax_head(0, sacc, pk0));
       barrier();  // K_1 landed in the prologue
     }
     // Block kb (buffer b = kb % 2), two matrix-core phases with VALU work
@@ -409,7 +370,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       if (kb >= kb_diag) mask(kb, sacc);
       pv(Buf<B ^ 1>{}, pk0, pk1);
       uint32_t pk0_next[8];
-      const float alpha = softmax_head(sacc, pk0_next);
+      const float alpha = softmax_head(kb, sacc, pk0_next);
       interleave<kDTiles * 4, 4, 4, kCopies>();
       rescale(alpha);
 #pragma unroll
@@ -437,7 +398,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     // ---- epilogue: full row sums, normalise, store ---------------------------
     l_run = halves_sum(l_run);
     if (wave_active && my_q < S) {
-      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+      const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
       const int64_t orow = (int64_t)my_q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
 #pragma unroll
       for (int dt = 0; dt < kDTiles; ++dt) {
@@ -465,15 +426,14 @@ hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stre
   const int GW = G < kWaves ? G : kWaves;
   const int pos_per_wg = kQB * (kWaves / GW);
   const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
-  const int nblk = (p.q_offset + p.seqlen + kKB - 1) / kKB;
-  const dim3 grid(nqb, p.kv_heads), vt_grid(nblk, p.kv_heads);
+  const dim3 grid(nqb, p.kv_heads);
+  const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder32, stream);
+  if (vt_rc != hipSuccess) return vt_rc;
   switch (head_dim) {
     case 128:
-      hipLaunchKernelGGL(prefill_vt_kernel<128>, vt_grid, dim3(256), 0, stream, p);
       hipLaunchKernelGGL(gqa_prefill_kernel<128>, grid, dim3(kWaves * 64), 0, stream, p);
       break;
     case 256:
-      hipLaunchKernelGGL(prefill_vt_kernel<256>, vt_grid, dim3(256), 0, stream, p);
       hipLaunchKernelGGL(gqa_prefill_kernel<256>, grid, dim3(kWaves * 64), 0, stream, p);
       break;
     default: return hipErrorInvalidValue;

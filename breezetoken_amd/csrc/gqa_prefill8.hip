@@ -71,9 +71,6 @@ __device__ __forceinline__ floatx4 mfma16_f16(const u32x4& a, const u32x4& b, co
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8_8, a), __builtin_bit_cast(halfx8_8, b), c,
                                                 0, 0, 0);
 }
-__device__ __forceinline__ uint32_t pack_rtz8(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
-}
 // Round to nearest even through a builtin (not asm), so the compiler sees the
 // VALU write and inserts the wait states an in-flight MFMA operand needs.
 __device__ __forceinline__ uint32_t pack_rne8(float a, float b) {
@@ -81,53 +78,6 @@ __device__ __forceinline__ uint32_t pack_rne8(float a, float b) {
 }
 
 }  // namespace
-
-// Pre-pass: V (S, Hkv, D) bf16 -> fp16 V^T image for the 16x16 MFMA layout.
-// Key block b of kv head g is stored at vt + (g * nblk + b) * 64 * D; chunk c =
-// kh*4 + q (kh: 32-key half, q: lane group) holds at row d the 8 values
-// V[b*64 + key][d], key = kh*32 + q*4 + {0, 1, 2, 3, 16, 17, 18, 19} (16 bytes).
-// Keys past the prompt are zero.  Each thread transposes 8 x 8 tiles.
-template <int D>
-__global__ __launch_bounds__(256) void prefill_vt8_kernel(PrefillParams p) {
-  constexpr int kDC = D / 8;
-  const int blk = blockIdx.x, g = blockIdx.y;
-  const int nblk = gridDim.x;
-  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-  const __amdgpu_buffer_rsrc_t vrs =
-      rsrc8(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)(p.q_offset + p.seqlen) * row_bytes);
-  uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kKB8 * D;
-  // The block's image (8 chunks x D rows x 16 bytes) is assembled in LDS and
-  // stored linearly, 1 KiB per wave instruction; a thread's own 8 output rows
-  // are 128 contiguous bytes, so storing them directly would touch 64 cache
-  // lines per instruction.  16-byte unit x sits in LDS slot x ^ ((x >> 3) & 7).
-  constexpr int kUnits = kKB8 * D * 2 / 16;
-  __shared__ __attribute__((aligned(16))) u32x4 stage[kUnits];
-  for (int item = threadIdx.x; item < 8 * kDC; item += 256) {
-    const int c = item / kDC, dc = item % kDC;
-    u32x4 rows[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int key = blk * kKB8 + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16;
-      rows[j] = load16_8(vrs, (uint32_t)key * row_bytes + (uint32_t)dc * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {  // output row d = dc*8 + i
-      u32x4 o;
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const uint32_t w0 = rows[2 * m][i >> 1], w1 = rows[2 * m + 1][i >> 1];
-        const float f0 = __uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16));
-        const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
-        o[m] = pack_rtz8(f0, f1);
-      }
-      const int x = c * D + dc * 8 + i;
-      stage[x ^ ((x >> 3) & 7)] = o;
-    }
-  }
-  __syncthreads();
-  u32x4* dst = reinterpret_cast<u32x4*>(img);
-  for (int x = threadIdx.x; x < kUnits; x += 256) dst[x] = stage[x ^ ((x >> 3) & 7)];
-}
 
 template <int D>
 __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillParams p) {
@@ -241,6 +191,8 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   for (int i = 0; i < kDTiles; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_ref = -INFINITY;          // reference max (log2 domain) of this lane's query column
   float l_run = 0.f;                // partial row sum over this lane's keys
+  int e_run = kVExpZero;            // V scale O is kept in: O_true = O * 2^e_run
+  const int* vexp = p.vexp + kvh * nblk;
   const int my_q = q0 + i16;
   const int my_pos = P0 + my_q;     // keys 0 .. my_pos
   u32x4 pk[2];                      // P of the pending block: 32-key halves, fp16
@@ -285,10 +237,12 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
         sacc[sub][r] = key <= my_pos ? sacc[sub][r] : -INFINITY;
       }
   };
-  // Online softmax of one block: max over the 64 keys of the column (this
+  // Online softmax of block kb: max over the 64 keys of the column (this
   // lane's 16 and three lane groups' via xor 16 / 32), lazy reference update,
   // P as fp16 in the MFMA key order; returns the factor O must be scaled by.
-  auto softmax = [&](floatx4 (&sacc)[4], u32x4 (&out)[2]) -> float {
+  // The V^T block's power-of-two scale enters P' = P * 2^shift through the
+  // exp2 bias; the row sum takes P.
+  auto softmax = [&](int kb, floatx4 (&sacc)[4], u32x4 (&out)[2]) -> float {
     float tmax = -INFINITY;
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub)
@@ -300,7 +254,10 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     const float m_new = move ? tmax : m_ref;
     const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
     m_ref = m_new;
-    const float neg_m = m_ref == -INFINITY ? 0.f : -m_ref;
+    const int eb = sload(vexp, kb);
+    const int e_new = vexp_next(e_run, eb);
+    const int shift = vexp_shift(e_new, eb);
+    const float neg_m = (m_ref == -INFINITY ? 0.f : -m_ref) + (float)shift;
     float psum = 0.f;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
@@ -313,8 +270,11 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
         out[kh][j] = pack_rne8(e0, e1);
       }
     }
+    if (shift != 0) psum = __builtin_ldexpf(psum, -shift);  // wave-uniform, rare
     l_run = l_run * alpha + psum;
-    return alpha;
+    const float factor = e_new != e_run ? __builtin_ldexpf(alpha, e_run - e_new) : alpha;
+    e_run = e_new;
+    return factor;
   };
   auto rescale = [&](float alpha) {
     if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max moved by > 2^8
@@ -340,7 +300,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     barrier();
     copy_k(Buf8<0>{}, min(kb0 + 2, last));
     if (kb0 >= kb_diag) mask(kb0, sacc);
-    softmax(sacc, pk);  // O is still zero: its factor does not matter
+    softmax(kb0, sacc, pk);  // O is still zero: its factor does not matter
     barrier();
   }
   // Block kb: A: S_kb = K_kb . Q^T; B: O += V_{kb-1} . P_{kb-1} beside the
@@ -356,7 +316,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     if (kb >= kb_diag) mask(kb, sacc);
     pv(Buf8<B ^ 1>{}, pk);
     u32x4 pk_next[2];
-    const float alpha = softmax(sacc, pk_next);
+    const float alpha = softmax(kb, sacc, pk_next);
     rescale(alpha);
     pk[0] = pk_next[0];
     pk[1] = pk_next[1];
@@ -386,7 +346,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     const int64_t slot = ((int64_t)kvh * nqb + qblk) * p.max_chunks + chunk;
     const int row = wave * kQ8 + i16;
     float* prow = p.part + (slot * kRows8 + row) * D;
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
 #pragma unroll
     for (int dt = 0; dt < kDTiles; ++dt) {
       const int d = dt * 16 + g4 * 4;
@@ -397,7 +357,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     return;
   }
   if (q0 < S && my_q < S) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
     const int64_t orow = (int64_t)my_q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
 #pragma unroll
     for (int dt = 0; dt < kDTiles; ++dt) {
@@ -533,19 +493,18 @@ bool prefill8_serves(int group, int head_dim) {
 hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t stream) {
   const int pos_per_wg = kQ8 * (kWaves8 / p.group);
   const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
-  const int nblk = (p.q_offset + p.seqlen + kKB8 - 1) / kKB8;
   const bool split = p.kb_chunk > 0;
   if (split && (p.max_chunks < 1 || p.max_chunks > kMaxChunks || !p.part || !p.lse)) return hipErrorInvalidValue;
-  const dim3 grid(nqb, p.kv_heads, split ? p.max_chunks : 1), vt_grid(nblk, p.kv_heads);
+  const dim3 grid(nqb, p.kv_heads, split ? p.max_chunks : 1);
   const dim3 cgrid(nqb, p.kv_heads, kRows8 * head_dim / 4 / 256);
+  const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder16, stream);
+  if (vt_rc != hipSuccess) return vt_rc;
   switch (head_dim) {
     case 128:
-      hipLaunchKernelGGL(prefill_vt8_kernel<128>, vt_grid, dim3(256), 0, stream, p);
       hipLaunchKernelGGL(gqa_prefill8_kernel<128>, grid, dim3(kWaves8 * 64), 0, stream, p);
       if (split) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
       break;
     case 256:
-      hipLaunchKernelGGL(prefill_vt8_kernel<256>, vt_grid, dim3(256), 0, stream, p);
       hipLaunchKernelGGL(gqa_prefill8_kernel<256>, grid, dim3(kWaves8 * 64), 0, stream, p);
       if (split) hipLaunchKernelGGL(prefill_combine_kernel<256>, cgrid, dim3(256), 0, stream, p);
       break;

@@ -68,85 +68,6 @@ __device__ __forceinline__ floatx4 mfma_f16(const u32x4& a, const u32x4& b, cons
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_p){a, b}, half2_p));
 }
-// Scalar (constant-cache) read of a value another kernel wrote.
-__device__ __forceinline__ int sload(const int* p, int i) {
-  return ((const __attribute__((address_space(4))) int*)(p))[i];
-}
-
-}  // namespace
-
-// Pre-pass: V (kv_len, Hkv, D) bf16 -> fp16 V^T image for 16x16x32 MFMAs,
-// one power-of-two scale per 64-key block.  Block b of kv head g: e =
-// 4 * ceil((E - 14) / 4), E the binary exponent of the block's largest |v| (e
-// = -128 for a block of zeros); the image holds v * 2^-e, so its largest
-// magnitude is in [2^11, 2^15) and no value overflows fp16 or loses
-// precision to fp16's subnormal range.  e goes to vexp[g * nblk + b].  Layout:
-// block b of head g at vt + (g * nblk + b) * 64 * D; chunk c = kh*4 + q (kh:
-// 32-key half, q: lane group) holds at row d the 8 values of keys kh*32 + q*4 +
-// {0, 1, 2, 3, 16, 17, 18, 19} (16 bytes), the order in which a 16x16 result's
-// lane group q holds P.  Keys past kv_len are zero.
-template <int D>
-__global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
-  constexpr int kDC = D / 8;                 // 16-byte column chunks per row
-  constexpr int kItems = 8 * kDC;            // (chunk, column chunk) items per block
-  static_assert(kItems <= 256, "one item per thread");
-  constexpr int kBlk = kPrefillKeyBlock;
-  const int blk = blockIdx.x, g = blockIdx.y;
-  const int nblk = gridDim.x;
-  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-  const __amdgpu_buffer_rsrc_t vrs =
-      rsrc_p(p.v + (int64_t)g * p.kv_stride_head, (uint32_t)(p.q_offset + p.seqlen) * row_bytes);
-  uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kBlk * D;
-  constexpr int kUnits = kBlk * D * 2 / 16;
-  __shared__ __attribute__((aligned(16))) u32x4 stage[kUnits];
-  __shared__ uint32_t wmax[4];
-  const int item = threadIdx.x;
-  const int c = item / kDC, dc = item % kDC;
-  u32x4 rows[8];
-  uint32_t mx = 0;  // largest |v| as bf16 bits (monotonic for finite values)
-  if (item < kItems) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int key = blk * kBlk + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16;
-      rows[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((uint32_t)key * row_bytes + (uint32_t)dc * 16), 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mx = max(mx, max(rows[j][i] & 0x7fffu, (rows[j][i] >> 16) & 0x7fffu));
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
-  int e = -128;
-  if (mx != 0) {
-    const int ebits = (int)(mx >> 7);                 // biased exponent (0: subnormal)
-    const int E = (ebits == 0 ? 1 : ebits) - 127;
-    e = -4 * ((14 - E) / 4);                          // 4 * ceil((E - 14) / 4) for E <= 14
-    if (E > 14) e = 4 * ((E - 14 + 3) / 4);
-  }
-  if (threadIdx.x == 0) p.vexp[g * nblk + blk] = e;
-  if (item < kItems) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {  // output row d = dc*8 + i
-      u32x4 o;
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const uint32_t w0 = rows[2 * m][i >> 1], w1 = rows[2 * m + 1][i >> 1];
-        const float f0 = __uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16));
-        const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
-        o[m] = pack_h2(__builtin_ldexpf(f0, -e), __builtin_ldexpf(f1, -e));
-      }
-      const int x = c * D + dc * 8 + i;
-      stage[x ^ ((x >> 3) & 7)] = o;
-    }
-  }
-  __syncthreads();
-  u32x4* dst = reinterpret_cast<u32x4*>(img);
-  for (int x = threadIdx.x; x < kUnits; x += 256) dst[x] = stage[x ^ ((x >> 3) & 7)];
-}
-
-namespace {
 
 // Shapes of the pair kernel's query blocks: a group covers 4 * NQT q-tiles of
 // 16 query positions each, for HG = min(G, 4 * NQT) heads of the kv group and
@@ -300,7 +221,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // ---- running state: per q-tile column (this lane's i16) -------------------
   floatx4 oacc[NQT][kDTiles];
   float m_ref[NQT], l_run[NQT];
-  int e_run = -128;   // scale exponent O is kept in: O_true = O * 2^e_run
+  int e_run = kVExpZero;  // scale exponent O is kept in: O_true = O * 2^e_run
   auto reset = [&]() {
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
@@ -309,7 +230,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       m_ref[t] = -INFINITY;
       l_run[t] = 0.f;
     }
-    e_run = -128;
+    e_run = kVExpZero;
   };
   const float c_log2 = p.scale_log2;
 
@@ -405,11 +326,12 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       }
     }
     // The V^T tile's scale: e of its 64-key block (wave-uniform).  P enters
-    // P.V as P' = P * 2^(eb - e_new) <= P (the shift rides in the exp2 bias);
-    // the row sum takes P, i.e. the sum of P' times 2^(e_new - eb).
+    // P.V as P' = P * 2^shift (the shift rides in the exp2 bias); the row sum
+    // takes P, i.e. the sum of P' times 2^-shift.
     const int eb = sload(vexp, key0 / kPrefillKeyBlock);
-    const int e_new = eb > e_run ? eb : e_run;
-    const float dshift = (float)(eb - e_new);
+    const int e_new = vexp_next(e_run, eb);
+    const int shift = vexp_shift(e_new, eb);
+    const float dshift = (float)shift;
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
       const floatx4& s0 = sacc[0][t];
@@ -429,7 +351,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
         e[4 + r] = fast_exp2(fmaf(s1[r], c_log2, bias));
       }
       float psum = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
-      if (e_new != eb) psum = __builtin_ldexpf(psum, e_new - eb);  // wave-uniform, rare
+      if (shift != 0) psum = __builtin_ldexpf(psum, -shift);  // wave-uniform, rare
       l_run[t] = l_run[t] * alpha + psum;
       if (e_new != e_run) alpha = __builtin_ldexpf(alpha, e_run - e_new);
       // Key order of the V^T chunk g4: keys g4*4 + {0..3}, 16 + g4*4 + {0..3}.
@@ -653,10 +575,10 @@ hipError_t launch_prefill_pair(const PrefillParams& p, int head_dim, hipStream_t
   const bool qf32 = p.q_f32 != 0;
   const PairShape sh = pair_shape(p.group, qf32);
   const int nqb = (p.seqlen + sh.pos - 1) / sh.pos;
-  const int nblk = (p.q_offset + p.seqlen + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
-  const dim3 grid((nqb + 1) / 2, p.kv_heads * sh.nsub), vt_grid(nblk, p.kv_heads);
+  const dim3 grid((nqb + 1) / 2, p.kv_heads * sh.nsub);
+  const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder16, stream);
+  if (vt_rc != hipSuccess) return vt_rc;
 #define BT_PAIR_LAUNCH(DIM)                                                                            \
-  hipLaunchKernelGGL(prefill_vts_kernel<DIM>, vt_grid, dim3(256), 0, stream, p);                      \
   if (qf32)                                                                                            \
     hipLaunchKernelGGL((gqa_prefill_pair_kernel<DIM, true>), grid, dim3(2 * kGWaves * 64), 0, stream, p); \
   else                                                                                                 \

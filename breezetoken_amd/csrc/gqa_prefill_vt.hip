@@ -1,0 +1,116 @@
+// Pre-pass of the prefill kernels: V (kv_len, Hkv, D) bf16 -> scaled fp16 V^T
+// image, one power-of-two scale per 64-key block.
+//
+// Block b of kv head g: e = 4 * ceil((E - 14) / 4), E the binary exponent of
+// the block's largest |v| (kVExpZero for a block of zeros).  The image holds
+// v * 2^-e (round to nearest even), so the block's largest magnitude lies in
+// [2^11, 2^15): no bf16 value overflows fp16, and values down to 2^-25 times
+// the block's largest stay normal fp16 numbers (11 significant bits).  e goes to vexp[g * nblk + b]; the attention kernels
+// fold it into P (see vexp_next in bt_common.h).
+//
+// Layout: block b of head g at vt + (g * nblk + b) * 64 * D as 8 key chunks;
+// chunk c holds at row d the 8 values V[b*64 + key][d] (16 bytes) of
+//   order kVtOrder16: key = (c/4)*32 + (c%4)*4 + {0, 1, 2, 3, 16, 17, 18, 19},
+//     the order in which lane group c%4 of a 16x16 MFMA result holds P of the
+//     32-key half c/4;
+//   order kVtOrder32: key = (c/2)*16 + (c%2)*4 + {0, 1, 2, 3, 8, 9, 10, 11},
+//     the order in which a 32x32 MFMA result's registers hold P of the 16-key
+//     step c/2 for lane half c%2.
+// Keys past kv_len are zero.  One thread per (chunk, 8-column slice)
+// transposes an 8 x 8 tile in registers; the block's image is assembled in
+// LDS and stored linearly (1 KiB per wave instruction): 16-byte unit x sits in
+// LDS slot x ^ ((x >> 3) & 7), conflict-free both ways.
+#include "bt_common.h"
+#include "bt_kernels.h"
+
+namespace bt {
+
+namespace {
+
+typedef _Float16 half2_v __attribute__((ext_vector_type(2)));
+typedef float float2_v __attribute__((ext_vector_type(2)));
+
+template <int D, int ORDER>
+__global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
+  constexpr int kDC = D / 8;                 // 16-byte column chunks per row
+  constexpr int kItems = 8 * kDC;            // (chunk, column chunk) items per block
+  static_assert(kItems <= 256, "one item per thread");
+  constexpr int kBlk = kPrefillKeyBlock;
+  const int blk = blockIdx.x, g = blockIdx.y;
+  const int nblk = gridDim.x;
+  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.v + (int64_t)g * p.kv_stride_head), (short)0,
+      (int)((uint32_t)(p.q_offset + p.seqlen) * row_bytes), 0x00020000);
+  uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kBlk * D;
+  constexpr int kUnits = kBlk * D * 2 / 16;
+  __shared__ __attribute__((aligned(16))) u32x4 stage[kUnits];
+  __shared__ uint32_t wmax[4];
+  const int item = threadIdx.x;
+  const int c = item / kDC, dc = item % kDC;
+  u32x4 rows[8];
+  uint32_t mx = 0;  // largest |v| as bf16 bits (monotonic in |v|)
+  if (item < kItems) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = ORDER == kVtOrder16 ? blk * kBlk + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16
+                                          : blk * kBlk + (c >> 1) * 16 + (c & 1) * 4 + (j & 3) + (j >> 2) * 8;
+      rows[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((uint32_t)key * row_bytes + (uint32_t)dc * 16), 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = max(mx, max(rows[j][i] & 0x7fffu, (rows[j][i] >> 16) & 0x7fffu));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  int e = kVExpZero;
+  if (mx != 0) {
+    const int ebits = (int)(mx >> 7);                 // biased exponent (0: subnormal)
+    const int E = (ebits == 0 ? 1 : ebits) - 127;
+    e = E <= 14 ? -4 * ((14 - E) / 4) : 4 * ((E - 14 + 3) / 4);  // 4 * ceil((E - 14) / 4)
+  }
+  if (threadIdx.x == 0) p.vexp[g * nblk + blk] = e;
+  if (item < kItems) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // output row d = dc*8 + i
+      u32x4 o;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t w0 = rows[2 * m][i >> 1], w1 = rows[2 * m + 1][i >> 1];
+        const float f0 = __uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16));
+        const float f1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
+        o[m] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                                (float2_v){__builtin_ldexpf(f0, -e), __builtin_ldexpf(f1, -e)}, half2_v));
+      }
+      const int x = c * D + dc * 8 + i;
+      stage[x ^ ((x >> 3) & 7)] = o;
+    }
+  }
+  __syncthreads();
+  u32x4* dst = reinterpret_cast<u32x4*>(img);
+  for (int x = threadIdx.x; x < kUnits; x += 256) dst[x] = stage[x ^ ((x >> 3) & 7)];
+}
+
+}  // namespace
+
+hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, int order, hipStream_t stream) {
+  const int nblk = (p.q_offset + p.seqlen + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
+  const dim3 grid(nblk, p.kv_heads);
+  if (order != kVtOrder16 && order != kVtOrder32) return hipErrorInvalidValue;
+  switch (head_dim) {
+    case 128:
+      if (order == kVtOrder16) hipLaunchKernelGGL((prefill_vts_kernel<128, kVtOrder16>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((prefill_vts_kernel<128, kVtOrder32>), grid, dim3(256), 0, stream, p);
+      break;
+    case 256:
+      if (order == kVtOrder16) hipLaunchKernelGGL((prefill_vts_kernel<256, kVtOrder16>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((prefill_vts_kernel<256, kVtOrder32>), grid, dim3(256), 0, stream, p);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace bt

@@ -75,10 +75,14 @@ def c3_inputs(valid: int, cap: int | None = None) -> DecodeCase:
     return decode_inputs(2, 16, 2, 256, cap or valid, valid, outlier_frac=0.01)
 
 
-def c4_inputs(steps: int):
-    """Config 4: causal prefill, H=8, Hkv=2, D=256, seed 3: q (S, 8, 256), k/v (S, 2, 256) bf16."""
+def c4_inputs(steps: int, q_f32: bool = False):
+    """Config 4: causal prefill, H=8, Hkv=2, D=256, seed 3: q (S, 8, 256) bf16
+    (or the same draws unrounded in f32, as the reference's prefill keeps q),
+    k/v (S, 2, 256) bf16."""
     g = torch.Generator().manual_seed(3)
-    q = torch.randn(steps, 8, 256, generator=g).to(torch.bfloat16)
+    q = torch.randn(steps, 8, 256, generator=g)
+    if not q_f32:
+        q = q.to(torch.bfloat16)
     k = torch.randn(steps, 2, 256, generator=g).to(torch.bfloat16)
     v = torch.randn(steps, 2, 256, generator=g).to(torch.bfloat16)
     return q, k, v, 256**-0.5

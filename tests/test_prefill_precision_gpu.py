@@ -1,0 +1,109 @@
+"""Prefill precision on the GPU: f32 q as the reference computes it, and V of
+any bf16 magnitude.
+
+* The reference keeps q in f32 through RMSNorm/RoPE into SDPA
+  (breezetoken/model/prefill.py:49-68).  bt_gqa_prefill takes that f32 q
+  (carried as a bf16 hi/lo pair through Q.K^T) and is held to the parity gate
+  (max-abs 2e-3, cosine 0.99999) against the oracle's f32 SDPA on the same
+  unrounded q.
+* V enters P.V as fp16 scaled by a power of two per 64-key block, so bf16 V
+  beyond fp16's range (|v| > 65504) or deep in its subnormals (|v| ~ 1e-5 and
+  below) must still match.  Each prefill kernel path is run on V patterns with
+  uniform, outlier-row, alternating-block, zero-block and falling magnitudes.
+  The gate scales with the data: |got - ref| <= 2e-3 * A(|V|) elementwise,
+  A(|V|) the oracle's attention over |V| (the magnitude each output averages;
+  for unit-variance V it is ~0.8, i.e. the usual 2e-3 gate), plus cosine
+  0.99999.  Magnitude changes fall on 64-key block boundaries: inside one
+  block the image keeps values down to 2^-25 of the block's largest (fp16's
+  normal range), so a row whose keys mix 1e-20 and 1e3 within one block
+  loses the small ones -- the one limit of the per-block scale.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from breezetoken_amd import workloads as wl
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+COS = 0.99999
+
+
+@pytest.mark.parametrize("steps", [128, 2048])
+def test_c4_prefill_f32_q_matches_reference_arithmetic(hip_backend, steps):
+    q, k, v, scale = wl.c4_inputs(steps, q_f32=True)
+    assert q.dtype == torch.float32
+    ref = orc.torch_prefill_attention(q, k.float(), v.float(), scale)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu()
+    err, cos = orc.compare(out.numpy(), ref.numpy())
+    print(f"[c4 f32 q] S={steps}: max-abs {err:.3e} cosine {cos:.9f}", flush=True)
+    assert err <= ATOL and cos >= COS
+
+
+def test_c4_prefill_f32_q_error_below_bf16_q(hip_backend):
+    """Carrying q as hi/lo must beat rounding it to bf16 (the error it removes)."""
+    q, k, v, scale = wl.c4_inputs(512, q_f32=True)
+    ref = orc.torch_prefill_attention(q, k.float(), v.float(), scale).numpy()
+    e32, _ = orc.compare(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu().numpy(), ref)
+    qb = q.to(torch.bfloat16)
+    e16, _ = orc.compare(hip_backend.attention_prefill(qb.cuda(), k.cuda(), v.cuda(), scale).cpu().numpy(), ref)
+    print(f"[c4 S=512] max-abs vs f32-q reference: f32 q {e32:.3e}, bf16 q {e16:.3e}", flush=True)
+    assert e32 < e16
+
+
+def _v_pattern(name: str, kv_len: int, kv: int, dim: int, g: torch.Generator) -> torch.Tensor:
+    v = torch.randn(kv_len, kv, dim, generator=g)
+    blk = torch.arange(kv_len) // 64
+    if name.startswith("uniform_"):
+        v = v * float(name.split("_")[1])
+    elif name == "outlier_rows_1e5":
+        v[::37] *= 1e5
+    elif name == "alternating_blocks":
+        v = v * torch.where(blk % 2 == 0, 1e3, 1e-3).view(-1, 1, 1)
+    elif name == "zero_blocks":
+        v[(blk == 0) | (blk == 2)] = 0.0
+    elif name == "big_then_tiny":
+        v = v * torch.where(blk < 2, 1e4, 1e-4).view(-1, 1, 1)
+    elif name == "tiny_then_big":
+        v = v * torch.where(blk < 2, 1e-20, 1e3).view(-1, 1, 1)
+    else:
+        raise ValueError(name)
+    return v.to(torch.bfloat16)
+
+
+V_PATTERNS = ["uniform_3e4", "uniform_1e5", "uniform_1e-5", "uniform_1e-30", "outlier_rows_1e5",
+              "alternating_blocks", "zero_blocks", "big_then_tiny", "tiny_then_big"]
+# (name, heads, kv, dim, steps, q_offset, q dtype, split_keys): the pair kernel
+# (f32 q), the two-waves-per-SIMD kernel alone and with split keys (bf16 q,
+# short prompt), the one-wave kernel (group size 3).
+PATHS = [
+    ("pair_f32q", 8, 2, 256, 320, 0, torch.float32, True),
+    ("prefill8", 8, 2, 256, 320, 0, torch.bfloat16, False),
+    ("prefill8_split", 8, 2, 128, 96, 640, torch.bfloat16, True),
+    ("onewave_g3", 6, 2, 128, 200, 0, torch.bfloat16, True),
+]
+
+
+@pytest.mark.parametrize("pattern", V_PATTERNS)
+@pytest.mark.parametrize("path", PATHS, ids=[p[0] for p in PATHS])
+def test_prefill_v_magnitudes(hip_backend, path, pattern):
+    name, heads, kv, dim, steps, pos0, qdt, split = path
+    print(f"[v-range] {name} {pattern}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(steps, heads, dim, generator=g).to(qdt)
+    k = torch.randn(pos0 + steps, kv, dim, generator=g).to(torch.bfloat16)
+    v = _v_pattern(pattern, pos0 + steps, kv, dim, g)
+    scale = dim**-0.5
+    ref = orc.torch_prefill_banded(q.float(), k.float(), v.float(), pos0, scale)
+    mag = orc.torch_prefill_banded(q.float(), k.float(), v.float().abs(), pos0, scale)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, q_offset=pos0, split_keys=split).cpu()
+    assert torch.isfinite(out).all(), "non-finite output"
+    excess = ((out - ref).abs() / (ATOL * mag).clamp_min(1e-38)).max().item()
+    _, cos = orc.compare(out.numpy().astype(np.float64), ref.numpy().astype(np.float64))
+    print(f"    error / (2e-3 * A(|V|)) max {excess:.3f}, cosine {cos:.9f}", flush=True)
+    assert excess <= 1.0 and cos >= COS
