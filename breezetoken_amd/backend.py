@@ -118,8 +118,6 @@ def prefill_unserved(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offset
         return "prefill needs token/head strides in positive multiples of 8 elements"
     if any(t.data_ptr() % 16 for t in (q, k, v)):
         return "prefill needs 16-byte aligned q/k/v"
-    if q.dtype == torch.float32 and heads // groups not in (1, 2, 4, 8):
-        return "f32 q is served for group sizes 1, 2, 4 and 8 (narrow q to bf16 for others)"
     nblk = -(-k.shape[0] // 64)
     if (nblk + 1) * 64 * k.stride(0) * 2 > 0xFFFFFFFF or nblk * 64 * dim * 2 > 0xFFFFFFFF:
         return "one kv head's K rows and V^T image must stay below 4 GiB"

@@ -124,4 +124,55 @@ __device__ __forceinline__ int sload(const int* p, int i) {
 // Power-of-two factor of a block's P: P' = P * 2^shift enters P.V.
 __device__ __forceinline__ int vexp_shift(int e_new, int eb) { return eb == kVExpZero ? 0 : eb - e_new; }
 
+// Prefill queries enter Q.K^T as fp16 scaled by 2^-e per query row (f32 or
+// bf16 q alike), e = E - 14 for the row's largest |q| (0 for a row of zeros).
+// Largest |q| of the 8 values at q + off (f32 or bf16 elements) as f32 bits,
+// which order like |q|.
+__device__ __forceinline__ uint32_t q_chunk_absmax(const void* q, bool f32, int64_t off) {
+  uint32_t mx = 0;
+  if (f32) {
+    const float* qf = reinterpret_cast<const float*>(q) + off;
+    const float4 a = *reinterpret_cast<const float4*>(qf);
+    const float4 b = *reinterpret_cast<const float4*>(qf + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = max(mx, __float_as_uint(v[i]) & 0x7fffffffu);
+  } else {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(q) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = max(mx, max((w[i] << 16) & 0x7fffffffu, w[i] & 0x7fff0000u));
+  }
+  return mx;
+}
+__device__ __forceinline__ int absmax_exp(uint32_t bits) {
+  if (bits == 0) return 0;
+  const int ebits = (int)(bits >> 23);
+  return (ebits == 0 ? 1 : ebits) - 127 - 14;
+}
+typedef _Float16 half2_c __attribute__((ext_vector_type(2)));
+typedef float float2_c __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_f16x2_scaled(float a, float b, int e) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector((float2_c){__builtin_ldexpf(a, -e), __builtin_ldexpf(b, -e)}, half2_c));
+}
+// The 8 values at q + off times 2^-e as an fp16 MFMA operand (round to nearest even).
+__device__ __forceinline__ u32x4 q_chunk_f16(const void* q, bool f32, int64_t off, int e) {
+  float v[8];
+  if (f32) {
+    const float* qf = reinterpret_cast<const float*>(q) + off;
+    const float4 a = *reinterpret_cast<const float4*>(qf);
+    const float4 b = *reinterpret_cast<const float4*>(qf + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(q) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  return u32x4{pack_f16x2_scaled(v[0], v[1], e), pack_f16x2_scaled(v[2], v[3], e),
+               pack_f16x2_scaled(v[4], v[5], e), pack_f16x2_scaled(v[6], v[7], e)};
+}
+
 }  // namespace bt

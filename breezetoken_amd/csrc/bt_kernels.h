@@ -57,7 +57,7 @@ struct CombineParams {
 };
 
 struct PrefillParams {
-  const uint16_t* q;   // bf16 (S, H, D) with strides
+  const uint16_t* q;   // (S, H, D) with strides, f32 or bf16 (q_f32)
   const uint16_t* k;   // bf16 (S, Hkv, D)
   const uint16_t* v;
   int64_t q_stride_tok, q_stride_head;
@@ -73,7 +73,9 @@ struct PrefillParams {
   int64_t out_stride_tok, out_stride_head;
   uint16_t* vt;        // workspace: fp16 V^T image, prefill_vt_bytes() bytes
   int32_t* vexp;       // workspace: per (kv head, 64-key block) power-of-two scale of the image
-  int32_t q_f32;       // 1: q is f32 (split into bf16 high and low parts), 0: bf16
+  uint16_t* kimg;      // workspace: fp16 K image (row-major, XOR-swizzled slots), prefill_vt_bytes() bytes
+  int32_t* kexp;       // workspace: per (kv head, 64-key block) power-of-two scale of the K image
+  int32_t q_f32;       // 1: q is f32, 0: bf16 (either enters Q.K^T as fp16 scaled per row)
   // Split-key mode of the two-waves-per-SIMD kernel (kb_chunk > 0): work-group
   // (query block, kv head, chunk c) covers key blocks [c*kb_chunk, +kb_chunk);
   // a query block with more than one chunk writes one normalised partial and
@@ -214,12 +216,13 @@ hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stre
 // Two-waves-per-SIMD prefill (gqa_prefill8.hip) for group sizes 1, 2, 4, 8.
 bool prefill8_serves(int group, int head_dim);
 // Pair kernel (gqa_prefill_pair.hip): two query blocks per work-group, 32
-// query columns per wave (16 with f32 q); group sizes 1, 2, 4, 8.
-bool prefill_pair_serves(int group, int head_dim, bool q_f32);
-int prefill_pair_grid(int seqlen, int group, int kv_heads, bool q_f32);
+// query columns per wave; group sizes 1, 2, 4, 8.
+bool prefill_pair_serves(int group, int head_dim);
+int prefill_pair_grid(int seqlen, int group, int kv_heads);
 hipError_t launch_prefill_pair(const PrefillParams& p, int head_dim, hipStream_t stream);
 // Scaled fp16 V^T image + per-block exponents (p.vt, p.vexp) in the key order
-// of the 16x16 (kVtOrder16) or 32x32 (kVtOrder32) MFMA result layout.
+// of the 16x16 (kVtOrder16) or 32x32 (kVtOrder32) MFMA result layout, and the
+// scaled fp16 K image + exponents (p.kimg, p.kexp).
 constexpr int kVtOrder16 = 0;
 constexpr int kVtOrder32 = 1;
 hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, int order, hipStream_t stream);

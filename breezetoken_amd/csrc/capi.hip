@@ -91,22 +91,33 @@ int device_cus() {
   return n;
 }
 
-// Prefill workspace: the fp16 V^T image, then (256-byte aligned) one int32
-// scale exponent per kv head and 64-key block.
-int64_t prefill_vexp_offset(int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
-  return align256((int64_t)bt::prefill_vt_bytes(kv_len, kv_heads, head_dim));
+// Prefill workspace, each part 256-byte aligned: the fp16 V^T image, one int32
+// scale exponent per kv head and 64-key block, the fp16 K image of the same
+// size, and its exponents.
+struct PrefillLayout {
+  int64_t vexp, kimg, kexp, bytes;
+};
+PrefillLayout prefill_layout(int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
+  const int64_t img = align256((int64_t)bt::prefill_vt_bytes(kv_len, kv_heads, head_dim));
+  const int64_t nblk = ((int64_t)kv_len + bt::kPrefillKeyBlock - 1) / bt::kPrefillKeyBlock;
+  const int64_t tab = align256(nblk * kv_heads * 4);
+  PrefillLayout l;
+  l.vexp = img;
+  l.kimg = l.vexp + tab;
+  l.kexp = l.kimg + img;
+  l.bytes = l.kexp + tab;
+  return l;
 }
 int64_t prefill_base_bytes(int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
-  const int64_t nblk = ((int64_t)kv_len + bt::kPrefillKeyBlock - 1) / bt::kPrefillKeyBlock;
-  return prefill_vexp_offset(kv_len, kv_heads, head_dim) + align256(nblk * kv_heads * 4);
+  return prefill_layout(kv_len, kv_heads, head_dim).bytes;
 }
 
 // Long prompts whose pair grid fills the device run the pair kernel (it needs
-// no split-key partials); f32 q always does.
-bool prefill_uses_pair(int32_t seqlen, int32_t heads, int32_t kv_heads, int32_t head_dim, bool q_f32) {
+// no split-key partials).
+bool prefill_uses_pair(int32_t seqlen, int32_t heads, int32_t kv_heads, int32_t head_dim) {
   const int group = heads / kv_heads;
-  if (!bt::prefill_pair_serves(group, head_dim, q_f32)) return false;
-  return q_f32 || bt::prefill_pair_grid(seqlen, group, kv_heads, false) >= device_cus();
+  if (!bt::prefill_pair_serves(group, head_dim)) return false;
+  return bt::prefill_pair_grid(seqlen, group, kv_heads) >= device_cus();
 }
 
 // The split-key plan bt_gqa_prefill uses for this shape on the current device
@@ -116,7 +127,7 @@ bt::PrefillSplitPlan prefill_plan(int32_t seqlen, int32_t q_offset, int32_t head
   *part_offset = align256(prefill_base_bytes(q_offset + seqlen, kv_heads, head_dim));
   const int group = heads / kv_heads;
   if (!bt::prefill8_serves(group, head_dim)) return bt::PrefillSplitPlan{};
-  if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim, false)) return bt::PrefillSplitPlan{};
+  if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim)) return bt::PrefillSplitPlan{};
   return bt::prefill8_split_plan(seqlen, q_offset, group, kv_heads, head_dim, device_cus());
 }
 
@@ -449,7 +460,6 @@ int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v,
       nblk * bt::kPrefillKeyBlock * head_dim * 2 > (int64_t)UINT32_MAX)
     return BT_ENOTSUP;
   const bool q_f32 = q_dtype == BT_DTYPE_F32;
-  if (q_f32 && !bt::prefill_pair_serves(heads / kv_heads, head_dim, true)) return BT_ENOTSUP;
   if (workspace_bytes < bt_prefill_workspace_bytes(kv_len, kv_heads, head_dim)) return BT_ENOSPC;
   bt::PrefillParams p{};
   p.q = static_cast<const uint16_t*>(q);
@@ -470,9 +480,12 @@ int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v,
   p.out_stride_tok = out_stride_tok;
   p.out_stride_head = out_stride_head;
   p.vt = static_cast<uint16_t*>(workspace);
-  p.vexp = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + prefill_vexp_offset(kv_len, kv_heads, head_dim));
+  const PrefillLayout lay = prefill_layout(kv_len, kv_heads, head_dim);
+  p.vexp = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + lay.vexp);
+  p.kimg = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + lay.kimg);
+  p.kexp = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + lay.kexp);
   p.q_f32 = q_f32 ? 1 : 0;
-  if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim, q_f32))
+  if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim))
     return hip_rc(bt::launch_prefill_pair(p, head_dim, (hipStream_t)stream));
   // Group sizes 1, 2, 4, 8 at D = 128 / 256 run two waves per SIMD; other
   // shapes take the one-wave-per-SIMD kernel.  Each writes its own fp16 V^T

@@ -10,19 +10,21 @@
 // Qwen36MoE._attn_batch (breezetoken/model/qwen36_moe.py:394-428).
 //
 // Decomposition (MI355X-first):
-//  * a small pre-pass (gqa_prefill_vt.hip, key order kVtOrder32) writes V
-//    once per kv head as a transposed fp16 image scaled by a power of two per
-//    64-key block, so the key loop needs neither a conversion nor a
-//    transposing LDS read, and every finite bf16 V fits fp16;
+//  * a small pre-pass (gqa_prefill_vt.hip, key order kVtOrder32) writes K and
+//    V once per kv head as fp16 images (V transposed), each scaled by a power
+//    of two per 64-key block, so the key loop needs neither a conversion nor
+//    a transposing LDS read, and every finite bf16 K and V fits fp16;
 //  * one work-group (4 waves) per (block of query positions, kv head); wave w
 //    owns query head w of the GQA group (and, for G < 4, a different block of
 //    positions), so every K/V tile staged in LDS feeds all G heads;
 //  * K and V^T tiles go HBM -> LDS by buffer_load ... lds (no staging
 //    registers, no LDS write instructions); K lands chunk-major (16-byte chunk
 //    c of key row r at c * 1024 + r * 16), which keeps the MFMA operand reads
-//    conflict-free and needs only a per-lane row offset on the HBM side;
-//  * S^T = K . Q^T on v_mfma_f32_32x32x16_bf16 (64 keys x 32 queries per
-//    block, Q^T in registers); O^T = V^T . P^T on v_mfma_f32_32x32x16_f16 with
+//    conflict-free and needs only a per-lane row offset into the image;
+//  * S^T = K . Q^T on v_mfma_f32_32x32x16_f16 (64 keys x 32 queries per
+//    block, Q^T in registers: q, f32 or bf16, scaled per row by a power of two
+//    and rounded to fp16; the softmax takes the q and K factors back in its
+//    exp2 argument); O^T = V^T . P^T on v_mfma_f32_32x32x16_f16 with
 //    P (<= 2^8, see below) rounded to fp16 -- bf16's 8-bit mantissa would put
 //    the first rows of the prompt above a 2e-3 error -- and the lane that owns
 //    a score column owns the P^T operand for it, so P never moves between lanes;
@@ -152,20 +154,21 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
   const int last = nkb - 1;
 
   // Tile copies.  K copy i (1 KiB) is 16-byte chunk i of the 64 key rows, lane
-  // l taking row l; V^T copy i is bytes [1024 i, +1024) of the block's image.
-  // Wave w issues copies w, w + 4, ...
-  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)nkeys * row_bytes);
+  // l taking row l, from the pre-pass's row-major fp16 K image (chunk i of row
+  // l sits in slot i ^ (l & 15)); V^T copy i is bytes [1024 i, +1024) of the
+  // block's image.  Wave w issues copies w, w + 4, ...
+  constexpr int kRowBytes = D * 2;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.kimg + (size_t)kvh * nblk * kKB * D, (uint32_t)nblk * kImg);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.vt + (size_t)kvh * nblk * kKB * D, (uint32_t)nblk * kImg);
   const int* vexp = p.vexp + kvh * nblk;
-  const uint32_t k_voff = (uint32_t)lane * row_bytes;
+  const int* kexp = p.kexp + kvh * nblk;
   const uint32_t v_voff = (uint32_t)lane * 16;
   auto copy_k = [&](auto b, int kb) {
-    const uint32_t so = (uint32_t)(kb * kKB) * row_bytes;
+    const uint32_t so = (uint32_t)kb * kImg;
 #pragma unroll
     for (int j = 0; j < kCopies; ++j) {
       const int i = wave + kWaves * j;
-      dma16(krs, k_buf(b) + i * 1024, k_voff, so + (uint32_t)i * 16);
+      dma16(krs, k_buf(b) + i * 1024, (uint32_t)lane * kRowBytes + (uint32_t)((i ^ (lane & 15)) * 16), so);
     }
   };
   auto copy_v = [&](auto b, int kb) {
@@ -192,7 +195,6 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
 
   const int qcol = lane & 31;       // this lane's query column
   const int kgrp = lane >> 5;       // k-slot group of MFMA operands
-  const float c_log2 = p.scale_log2;
 
   const int passes = (G + kWaves - 1) / kWaves;
   for (int pass = 0; pass < passes; ++pass) {
@@ -204,13 +206,24 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     const int head = kvh * G + min(head_local, G - 1);
 
     // ---- Q^T operand in registers: lane holds Q[q0 + qcol][d = st*16 + kgrp*8 .. +8]
+    // as fp16, the row scaled by 2^-eq so its largest |q| lies in [2^14,
+    // 2^15); c_col = scale * log2(e) * 2^eq restores it in the exp2 argument.
     u32x4 qop[kSteps];
+    float c_col;
     {
       const int qrow = min(q0 + qcol, S - 1);
-      const uint16_t* qp = p.q + (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + kgrp * 8;
+      const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + kgrp * 8;
+      const bool f32 = p.q_f32 != 0;
+      uint32_t mx = 0;
 #pragma unroll
-      for (int st = 0; st < kSteps; ++st) qop[st] = *reinterpret_cast<const u32x4*>(qp + st * 16);
+      for (int st = 0; st < kSteps; ++st) mx = max(mx, q_chunk_absmax(p.q, f32, off + st * 16));
+      mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));  // the row's two lane halves
+      const int eq = absmax_exp(mx);
+      c_col = __builtin_ldexpf(p.scale_log2, eq);
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) qop[st] = q_chunk_f16(p.q, f32, off + st * 16, eq);
     }
+    float c_blk = c_col;  // log2-domain factor of the latest block's scaled scores
 
     floatx16 oacc[kDTiles];
 #pragma unroll
@@ -242,7 +255,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const u32x4 a = *reinterpret_cast<const u32x4*>(krow + st * 2048 + mt * 512);
-          sacc[mt] = mfma32(as_bf16x8(a), as_bf16x8(qop[st]), sacc[mt]);
+          sacc[mt] = mfma32_f16(a, qop[st], sacc[mt]);
         }
       }
     };
@@ -278,8 +291,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       float psum = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; j += 2) {
-        const float p0 = fast_exp2(fmaf(s[j], c_log2, neg_m));
-        const float p1 = fast_exp2(fmaf(s[j + 1], c_log2, neg_m));
+        const float p0 = fast_exp2(fmaf(s[j], c_blk, neg_m));
+        const float p1 = fast_exp2(fmaf(s[j + 1], c_blk, neg_m));
         psum += p0 + p1;
         out[j / 2] = pack_f16_rne(p0, p1);
       }
@@ -297,7 +310,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int j = 0; j < 16; ++j) tmax = fmaxf(tmax, sacc[mt][j]);
-      tmax = halves_max(tmax) * c_log2;
+      c_blk = __builtin_ldexpf(c_col, sload(kexp, kb));  // with the K block's scale
+      tmax = halves_max(tmax) * c_blk;
       // lazy reference max: move it only when a score exceeds it by > kLazy
       const bool move = tmax > m_ref + kLazy;
       const float m_new = move ? tmax : m_ref;

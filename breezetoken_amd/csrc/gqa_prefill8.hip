@@ -1,4 +1,4 @@
-// Causal GQA prefill on CDNA4 bf16/f16 MFMA with two waves per SIMD.
+// Causal GQA prefill on CDNA4 fp16 MFMA with two waves per SIMD.
 //
 // Same contract as gqa_prefill.hip (the causal SDPA of prefill.py:56-68 and
 // the banded chunked prefill of qwen36_moe.py:394-428: query row i at
@@ -7,20 +7,21 @@
 //  * a work-group of 8 waves shares one K tile and one V^T tile in LDS; wave w
 //    owns query head (w % G) of the kv group and 16 query positions
 //    [q0 + (w / G) * 16, +16), G in {1, 2, 4, 8};
-//  * per 64-key block a wave runs 32 v_mfma_f32_16x16x32_bf16 for S^T = K.Q^T
-//    (K from LDS, Q^T in registers) and 32 v_mfma_f32_16x16x32_f16 for
-//    O^T += V^T.P^T (V^T from LDS, P^T built in registers from the S^T
-//    accumulators).  Per wave that is 64 accumulators of O, 32 registers of Q
-//    and 16 of S -- half of the one-wave-per-SIMD layout -- so two waves fit
-//    in the register file and hide each other's LDS, copy and barrier waits;
-//  * the K tile lands in LDS row-major with an XOR swizzle: 16-byte chunk c of
-//    key row r sits in slot c ^ (r & 15) of the row.  Each copy instruction
-//    then reads whole contiguous rows from HBM/L2 (the swizzle is applied on
-//    the source side: lane l of a copy fetches the chunk that belongs in its
-//    slot), and the operand reads of 16 consecutive rows hit 16 different
-//    bank groups;
-//  * the V^T image (fp16) holds each 64-key block as 8 chunks of 8 keys; chunk
-//    c = kh*4 + g holds keys kh*32 + g*4 + {0,1,2,3} and kh*32 + 16 + g*4 +
+//  * per 64-key block a wave runs 32 v_mfma_f32_16x16x32_f16 for S^T = K.Q^T
+//    (K from LDS, Q^T in registers) and 32 for O^T += V^T.P^T (V^T from LDS,
+//    P^T built in registers from the S^T accumulators).  Per wave that is 64
+//    accumulators of O, 32 registers of Q and 16 of S -- half of the
+//    one-wave-per-SIMD layout -- so two waves fit in the register file and
+//    hide each other's LDS, copy and barrier waits;
+//  * q (f32 or bf16) enters as fp16 with a power-of-two scale per query row,
+//    K and V come from the pre-pass's fp16 images (gqa_prefill_vt.hip), each
+//    scaled per 64-key block; the softmax takes all three factors back
+//    exactly in its exp2 argument;
+//  * the K image is row-major with 16-byte chunk c of key row r in slot c ^
+//    (r & 15), so a tile copy is contiguous and the operand reads of 16
+//    consecutive rows hit 16 different bank groups;
+//  * the V^T image holds each 64-key block as 8 chunks of 8 keys; chunk c =
+//    kh*4 + g holds keys kh*32 + g*4 + {0,1,2,3} and kh*32 + 16 + g*4 +
 //    {0,1,2,3}: the order in which lane group g of the 16x16 result registers
 //    holds P for the 32-key half kh, so the P^T operand never moves between
 //    lanes;
@@ -62,10 +63,6 @@ __device__ __forceinline__ u32x4 load16_8(__amdgpu_buffer_rsrc_t r, uint32_t vof
 __device__ __forceinline__ void dma16_8(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff,
                                         uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (BT_LDS void*)lds, 16, (int)voff, (int)soff, 0, 0);
-}
-__device__ __forceinline__ floatx4 mfma16_bf16(const u32x4& a, const u32x4& b, const floatx4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                 0, 0, 0);
 }
 __device__ __forceinline__ floatx4 mfma16_f16(const u32x4& a, const u32x4& b, const floatx4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8_8, a), __builtin_bit_cast(halfx8_8, b), c,
@@ -128,30 +125,19 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   const int last = kb1 - 1;
   const int head = kvh * G + wave % G;
 
-  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-  const __amdgpu_buffer_rsrc_t krs = rsrc8(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)nkeys * row_bytes);
+  const __amdgpu_buffer_rsrc_t krs = rsrc8(p.kimg + (size_t)kvh * nblk * kKB8 * D, (uint32_t)nblk * kImg);
   const __amdgpu_buffer_rsrc_t vrs = rsrc8(p.vt + (size_t)kvh * nblk * kKB8 * D, (uint32_t)nblk * kImg);
-  constexpr int kSlots = D / 8;                // 16-byte chunks per key row
-  constexpr int kRowsPerCopy = 64 / kSlots;    // key rows per 1 KiB copy
-  static_assert(kSlots >= 16, "the row swizzle uses 16 slots");
+  const int* kexp = p.kexp + kvh * nblk;
   const uint32_t v_voff = (uint32_t)lane * 16;
-  // K copy i (1 KiB) fills rows kRowsPerCopy*i .. of the tile: lane l fetches,
-  // for its slot s = l % kSlots of row r, the chunk s ^ (r & 15).  V^T copy i
-  // is bytes [1024 i, +1024) of the block's image.  Wave w issues copies w,
-  // w + 8, ...
-  uint32_t k_voff[kCopies];
-#pragma unroll
-  for (int j = 0; j < kCopies; ++j) {
-    const int r = (wave + kWaves8 * j) * kRowsPerCopy + lane / kSlots;
-    const int slot = lane % kSlots;
-    k_voff[j] = (uint32_t)r * row_bytes + (uint32_t)(slot ^ (r & 15)) * 16;
-  }
+  // Tile copy i (1 KiB) is bytes [1024 i, +1024) of the block's K or V^T
+  // image; the K image is row-major with 16-byte slot s of row r holding chunk
+  // s ^ (r & 15), so the tile lands swizzled.  Wave w issues copies w, w + 8, ...
   auto copy_k = [&](auto b, int kb) {
-    const uint32_t so = (uint32_t)(kb * kKB8) * row_bytes;
+    const uint32_t so = (uint32_t)kb * kImg;
 #pragma unroll
     for (int j = 0; j < kCopies; ++j) {
       const int i = wave + kWaves8 * j;
-      dma16_8(krs, k_buf(b) + i * 1024, k_voff[j], so);
+      dma16_8(krs, k_buf(b) + i * 1024, v_voff, so + (uint32_t)i * 1024);
     }
   };
   auto copy_v = [&](auto b, int kb) {
@@ -175,15 +161,25 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
 
   const int i16 = lane & 15;   // query column of the 16x16 tiles
   const int g4 = lane >> 4;    // lane group: k slice of the operands, rows 4*g4.. of results
-  const float c_log2 = p.scale_log2;
 
-  // Q^T operand: lane holds Q[q0 + i16][st*32 + g4*8 .. +8] for each 32-d step.
+  // Q^T operand: lane holds Q[q0 + i16][st*32 + g4*8 .. +8] for each 32-d step
+  // as fp16, the row scaled by 2^-eq so its largest |q| lies in [2^14, 2^15);
+  // c_col = scale * log2(e) * 2^eq restores it in the exp2 argument.
   u32x4 qop[kDSteps];
+  float c_col;
   {
     const int qrow = min(q0 + i16, S - 1);
-    const uint16_t* qp = p.q + (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + g4 * 8;
+    const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + g4 * 8;
+    const bool f32 = p.q_f32 != 0;
+    uint32_t mx = 0;
 #pragma unroll
-    for (int st = 0; st < kDSteps; ++st) qop[st] = *reinterpret_cast<const u32x4*>(qp + st * 32);
+    for (int st = 0; st < kDSteps; ++st) mx = max(mx, q_chunk_absmax(p.q, f32, off + st * 32));
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+    const int eq = absmax_exp(mx);
+    c_col = __builtin_ldexpf(p.scale_log2, eq);
+#pragma unroll
+    for (int st = 0; st < kDSteps; ++st) qop[st] = q_chunk_f16(p.q, f32, off + st * 32, eq);
   }
 
   floatx4 oacc[kDTiles];
@@ -209,7 +205,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       for (int sub = 0; sub < 4; ++sub) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(kb_ + (sub * 16 + i16) * (D * 2) +
                                                           (((st * 4 + g4) ^ i16) * 16));
-        sacc[sub] = mfma16_bf16(a, qop[st], st == 0 ? zero : sacc[sub]);
+        sacc[sub] = mfma16_f16(a, qop[st], st == 0 ? zero : sacc[sub]);
       }
     }
   };
@@ -248,6 +244,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
       for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[sub][r]);
+    const float c_log2 = __builtin_ldexpf(c_col, sload(kexp, kb));  // with the K block's scale
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = halves_max(tmax) * c_log2;
     const bool move = tmax > m_ref + kLazy8;

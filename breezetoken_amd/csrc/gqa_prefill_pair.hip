@@ -19,13 +19,15 @@
 //    keys of block N-1-j; B runs the remaining keys of block N-1-j; both take
 //    ceil((N+1)/2) steps in lockstep (one barrier per step), and the two
 //    halves of block N-1-j are merged through LDS at the end;
-//  * with f32 q (the reference keeps q in f32, prefill.py:49-68) a wave holds
-//    16 query columns and multiplies each K fragment with the bf16 high and
-//    low parts of q into the same accumulator: Q.K^T keeps ~16 mantissa bits;
+//  * Q.K^T runs on fp16 MFMAs: q (f32, as the reference keeps it through
+//    prefill.py:49-68, or bf16) is rounded to fp16 after scaling each query
+//    row by a power of two, and K comes from the pre-pass's fp16 image, scaled
+//    per 64-key block (gqa_prefill_vt.hip); both factors return exactly in the
+//    exp2 argument.  fp16's 11 bits keep q's rounding error 8x below bf16's;
 //  * P and V^T enter the P.V product as fp16 (P <= 2^8 from the lazily
 //    rescaled softmax); each 64-key block of V is stored scaled by its own
-//    power of two (prefill_vts_kernel), which the softmax folds into P, so V
-//    of any bf16 magnitude keeps fp16's 11 bits.
+//    power of two, which the softmax folds into P, so V of any bf16
+//    magnitude keeps fp16's 11 bits.
 #include "bt_common.h"
 #include "bt_kernels.h"
 
@@ -55,10 +57,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_p(const void* base, uint3
 __device__ __forceinline__ void dma16_p(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (BT_LDS void*)lds, 16, (int)voff, (int)soff, 0, 0);
 }
-__device__ __forceinline__ floatx4 mfma_bf16(const u32x4& a, const u32x4& b, const floatx4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
-                                                 0, 0);
-}
 __device__ __forceinline__ floatx4 mfma_f16(const u32x4& a, const u32x4& b, const floatx4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8_p, a), __builtin_bit_cast(halfx8_p, b), c,
                                                 0, 0, 0);
@@ -76,9 +74,9 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 struct PairShape {
   int nqt, hg, pos, nsub;
 };
-__host__ __device__ inline PairShape pair_shape(int group, bool qf32) {
+__host__ __device__ inline PairShape pair_shape(int group) {
   PairShape s;
-  s.nqt = qf32 ? 1 : 2;
+  s.nqt = 2;
   s.hg = group < 4 * s.nqt ? group : 4 * s.nqt;
   s.pos = 16 * 4 * s.nqt / s.hg;
   s.nsub = group / s.hg;
@@ -95,23 +93,22 @@ struct Sel {
   static constexpr bool value = B;
 };
 
-template <int D, bool QF32, int GRP, typename XB>
+template <int D, int GRP, typename XB>
 __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char* K0, unsigned char* K1,
                                            unsigned char* V0, unsigned char* V1, XB xbuf, float* xs) {
-  constexpr int NQT = QF32 ? 1 : 2;
+  constexpr int NQT = 2;
   constexpr int kDSteps = D / 32;
   constexpr int kDTiles = D / 16;
   constexpr int kRowBytes = D * 2;
   constexpr int kTile = kUnit * kRowBytes;           // 16 KiB at D = 256
   constexpr int kCopies = kTile / 1024 / kGWaves;    // 1 KiB copies per wave per tile
   static_assert(kCopies >= 1, "head_dim 128 or 256");
-  constexpr int kQParts = QF32 ? 2 : 1;              // hi and lo parts of q
 
   const int lane = threadIdx.x & 63;
   const int gw = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) & 3);
   const int i16 = lane & 15;
   const int g4 = lane >> 4;
-  const PairShape sh = pair_shape(p.group, QF32);
+  const PairShape sh = pair_shape(p.group);
   const int kvh = (int)blockIdx.y / sh.nsub;
   const int sub = (int)blockIdx.y % sh.nsub;
   const int S = p.seqlen;
@@ -142,27 +139,23 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   auto unit_key = [&](int st) { return GRP == 0 ? (st < sw ? st - lead : nb - xa + st - sw) : st; };
 
   const int nblk64 = (nkeys + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
-  const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-  const __amdgpu_buffer_rsrc_t krs = rsrc_p(p.k + (int64_t)kvh * p.kv_stride_head, (uint32_t)nkeys * row_bytes);
-  const __amdgpu_buffer_rsrc_t vrs =
-      rsrc_p(p.vt + (size_t)kvh * nblk64 * kPrefillKeyBlock * D, (uint32_t)nblk64 * kPrefillKeyBlock * kRowBytes);
+  const uint32_t img_bytes = (uint32_t)nblk64 * kPrefillKeyBlock * kRowBytes;
+  const __amdgpu_buffer_rsrc_t krs = rsrc_p(p.kimg + (size_t)kvh * nblk64 * kPrefillKeyBlock * D, img_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = rsrc_p(p.vt + (size_t)kvh * nblk64 * kPrefillKeyBlock * D, img_bytes);
   const int* vexp = p.vexp + kvh * nblk64;
+  const int* kexp = p.kexp + kvh * nblk64;
 
-  // K copy j (1 KiB, rows 2j, 2j+1 at D = 256): lane l fetches, for slot s of
-  // row r, chunk s ^ (r & 15) -- the K tile lands row-major with an XOR
-  // swizzle, so the operand reads of 16 consecutive rows hit 16 bank groups.
-  constexpr int kSlots = D / 8;
-  constexpr int kRowsPerCopy = 1024 / kRowBytes;
-  auto k_voff = [&](int j) -> uint32_t {  // recomputed per copy: registers are scarce
-    const int r = (gw * kCopies + j) * kRowsPerCopy + lane / kSlots;
-    return (uint32_t)(lane / kSlots) * row_bytes + (uint32_t)((lane % kSlots) ^ (r & 15)) * 16;
-  };
+  // Tile copies: the unit's 32 rows of K (row-major, slots XOR-swizzled by
+  // the pre-pass, so the operand reads of 16 consecutive rows hit 16 bank
+  // groups) and its V^T half-block are each 16 KiB contiguous in the images.
   auto copy_k = [&](unsigned char* kbuf, int u) {
     const int key0 = unit_key(u) * kUnit;
+    const uint32_t ksrc = (uint32_t)key0 * kRowBytes;
 #pragma unroll
-    for (int j = 0; j < kCopies; ++j)
-      dma16_p(krs, kbuf + (gw * kCopies + j) * 1024, k_voff(j),
-              (uint32_t)(key0 + (gw * kCopies + j) * kRowsPerCopy) * row_bytes);
+    for (int j = 0; j < kCopies; ++j) {
+      const int i = gw * kCopies + j;
+      dma16_p(krs, kbuf + i * 1024, (uint32_t)lane * 16, ksrc + (uint32_t)i * 1024);
+    }
   };
   auto copy_v = [&](unsigned char* vbuf, int u) {
     const int key0 = unit_key(u) * kUnit;
@@ -187,34 +180,27 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     head[t] = kvh * p.group + sub * sh.hg + qt % sh.hg;
     poff[t] = 16 * (qt / sh.hg);
   }
-  // Q^T operand: lane (i16, g4) holds q[row][st*32 + g4*8 .. +8] of column i16.
-  // Rows past the prompt read the last row (their output is not stored).
-  u32x4 qop[NQT][kQParts][kDSteps];
+  // Q^T operand: lane (i16, g4) holds q[row][st*32 + g4*8 .. +8] of column i16
+  // as fp16, scaled by 2^-eq so the row's largest |q| lies in [2^14, 2^15);
+  // c_col = scale * log2(e) * 2^eq restores it in the exp2 argument.  Rows
+  // past the prompt read the last row (their output is not stored).
+  u32x4 qop[NQT][kDSteps];
+  float c_col[NQT];
   auto load_q = [&](int blk) {
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
       const int row = min(blk * sh.pos + poff[t] + i16, S - 1);
       const int64_t off = (int64_t)row * p.q_stride_tok + (int64_t)head[t] * p.q_stride_head + g4 * 8;
+      const bool f32 = p.q_f32 != 0;
+      uint32_t mx = 0;
 #pragma unroll
-      for (int st = 0; st < kDSteps; ++st) {
-        if constexpr (QF32) {
-          const float* qf = reinterpret_cast<const float*>(p.q) + off + st * 32;
-          const float4 a = *reinterpret_cast<const float4*>(qf);
-          const float4 b = *reinterpret_cast<const float4*>(qf + 4);
-          const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-          uint32_t hi[8], lo[8];
+      for (int st = 0; st < kDSteps; ++st) mx = max(mx, q_chunk_absmax(p.q, f32, off + st * 32));
+      mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
+      mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+      const int eq = absmax_exp(mx);
+      c_col[t] = __builtin_ldexpf(p.scale_log2, eq);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            hi[i] = f32_to_bf16_bits(v[i]);
-            lo[i] = f32_to_bf16_bits(v[i] - bf16_bits_to_f32(hi[i]));
-          }
-          qop[t][0][st] = u32x4{pack2(hi[0], hi[1]), pack2(hi[2], hi[3]), pack2(hi[4], hi[5]), pack2(hi[6], hi[7])};
-          qop[t][kQParts - 1][st] =
-              u32x4{pack2(lo[0], lo[1]), pack2(lo[2], lo[3]), pack2(lo[4], lo[5]), pack2(lo[6], lo[7])};
-        } else {
-          qop[t][0][st] = *reinterpret_cast<const u32x4*>(p.q + off + st * 32);
-        }
-      }
+      for (int st = 0; st < kDSteps; ++st) qop[t][st] = q_chunk_f16(p.q, f32, off + st * 32, eq);
     }
   };
 
@@ -232,7 +218,6 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     }
     e_run = kVExpZero;
   };
-  const float c_log2 = p.scale_log2;
 
   // Normalise and store a finished block (rows past the prompt are skipped).
   auto store = [&](int blk, const float (&lsum)[NQT]) {
@@ -304,12 +289,10 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       }
       const u32x4 a0 = kf[st % (KLA + 1)][0], a1 = kf[st % (KLA + 1)][1];
 #pragma unroll
-      for (int t = 0; t < NQT; ++t)
-#pragma unroll
-        for (int h = 0; h < kQParts; ++h) {
-          sacc[0][t] = mfma_bf16(a0, qop[t][h][st], sacc[0][t]);
-          sacc[1][t] = mfma_bf16(a1, qop[t][h][st], sacc[1][t]);
-        }
+      for (int t = 0; t < NQT; ++t) {
+        sacc[0][t] = mfma_f16(a0, qop[t][st], sacc[0][t]);
+        sacc[1][t] = mfma_f16(a1, qop[t][st], sacc[1][t]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     // Causal mask: key key0 + kt*16 + g4*4 + r against this column's position.
@@ -329,6 +312,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     // P.V as P' = P * 2^shift (the shift rides in the exp2 bias); the row sum
     // takes P, i.e. the sum of P' times 2^-shift.
     const int eb = sload(vexp, key0 / kPrefillKeyBlock);
+    const int ek = sload(kexp, key0 / kPrefillKeyBlock);  // the K block's scale
     const int e_new = vexp_next(e_run, eb);
     const int shift = vexp_shift(e_new, eb);
     const float dshift = (float)shift;
@@ -336,6 +320,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     for (int t = 0; t < NQT; ++t) {
       const floatx4& s0 = sacc[0][t];
       const floatx4& s1 = sacc[1][t];
+      const float c_log2 = __builtin_ldexpf(c_col[t], ek);  // log2-domain factor of the scaled scores
       float tmax = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
       tmax = rows16_max(tmax);
       tmax = halves_max(tmax) * c_log2;
@@ -529,10 +514,10 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
 
 }  // namespace
 
-template <int D, bool QF32>
+template <int D>
 __global__ __launch_bounds__(2 * kGWaves * 64, 1) void gqa_prefill_pair_kernel(PrefillParams p) {
   constexpr int kTile = kUnit * D * 2;
-  constexpr int NQT = QF32 ? 1 : 2;
+  constexpr int NQT = 2;
   // Eight tile buffers (two per group per stage); after the key loop group A
   // hands its partial to group B through the first ones.
   __shared__ __attribute__((aligned(1024))) unsigned char kA0[kTile], kA1[kTile], vA0[kTile], vA1[kTile];
@@ -554,41 +539,36 @@ __global__ __launch_bounds__(2 * kGWaves * 64, 1) void gqa_prefill_pair_kernel(P
     return reinterpret_cast<float*>(b);
   };
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  if (wave < kGWaves) pair_group<D, QF32, 0>(p, kA0, kA1, vA0, vA1, xbuf, xs);
-  else pair_group<D, QF32, 1>(p, kB0, kB1, vB0, vB1, xbuf, xs);
+  if (wave < kGWaves) pair_group<D, 0>(p, kA0, kA1, vA0, vA1, xbuf, xs);
+  else pair_group<D, 1>(p, kB0, kB1, vB0, vB1, xbuf, xs);
 }
 
-bool prefill_pair_serves(int group, int head_dim, bool q_f32) {
+bool prefill_pair_serves(int group, int head_dim) {
   if (head_dim != 128 && head_dim != 256) return false;
-  if (group != 1 && group != 2 && group != 4 && group != 8) return false;
-  (void)q_f32;
-  return true;
+  return group == 1 || group == 2 || group == 4 || group == 8;
 }
 
-int prefill_pair_grid(int seqlen, int group, int kv_heads, bool q_f32) {
-  const PairShape sh = pair_shape(group, q_f32);
+int prefill_pair_grid(int seqlen, int group, int kv_heads) {
+  const PairShape sh = pair_shape(group);
   const int nqb = (seqlen + sh.pos - 1) / sh.pos;
   return ((nqb + 1) / 2) * kv_heads * sh.nsub;
 }
 
 hipError_t launch_prefill_pair(const PrefillParams& p, int head_dim, hipStream_t stream) {
-  const bool qf32 = p.q_f32 != 0;
-  const PairShape sh = pair_shape(p.group, qf32);
+  const PairShape sh = pair_shape(p.group);
   const int nqb = (p.seqlen + sh.pos - 1) / sh.pos;
   const dim3 grid((nqb + 1) / 2, p.kv_heads * sh.nsub);
   const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder16, stream);
   if (vt_rc != hipSuccess) return vt_rc;
-#define BT_PAIR_LAUNCH(DIM)                                                                            \
-  if (qf32)                                                                                            \
-    hipLaunchKernelGGL((gqa_prefill_pair_kernel<DIM, true>), grid, dim3(2 * kGWaves * 64), 0, stream, p); \
-  else                                                                                                 \
-    hipLaunchKernelGGL((gqa_prefill_pair_kernel<DIM, false>), grid, dim3(2 * kGWaves * 64), 0, stream, p);
   switch (head_dim) {
-    case 128: BT_PAIR_LAUNCH(128) break;
-    case 256: BT_PAIR_LAUNCH(256) break;
+    case 128:
+      hipLaunchKernelGGL(gqa_prefill_pair_kernel<128>, grid, dim3(2 * kGWaves * 64), 0, stream, p);
+      break;
+    case 256:
+      hipLaunchKernelGGL(gqa_prefill_pair_kernel<256>, grid, dim3(2 * kGWaves * 64), 0, stream, p);
+      break;
     default: return hipErrorInvalidValue;
   }
-#undef BT_PAIR_LAUNCH
   return hipGetLastError();
 }
 

@@ -1,25 +1,36 @@
-// Pre-pass of the prefill kernels: V (kv_len, Hkv, D) bf16 -> scaled fp16 V^T
-// image, one power-of-two scale per 64-key block.
+// Pre-pass of the prefill kernels: K and V (kv_len, Hkv, D) bf16 -> scaled
+// fp16 images, one power-of-two scale per 64-key block of each.
 //
-// Block b of kv head g: e = 4 * ceil((E - 14) / 4), E the binary exponent of
-// the block's largest |v| (kVExpZero for a block of zeros).  The image holds
-// v * 2^-e (round to nearest even), so the block's largest magnitude lies in
-// [2^11, 2^15): no bf16 value overflows fp16, and values down to 2^-25 times
-// the block's largest stay normal fp16 numbers (11 significant bits).  e goes to vexp[g * nblk + b]; the attention kernels
-// fold it into P (see vexp_next in bt_common.h).
-//
-// Layout: block b of head g at vt + (g * nblk + b) * 64 * D as 8 key chunks;
-// chunk c holds at row d the 8 values V[b*64 + key][d] (16 bytes) of
+// V^T image, block b of kv head g: e = 4 * ceil((E - 14) / 4), E the binary
+// exponent of the block's largest |v| (kVExpZero for a block of zeros).  The
+// image holds v * 2^-e (round to nearest even), so the block's largest
+// magnitude lies in [2^11, 2^15): no bf16 value overflows fp16, and values
+// down to 2^-25 times the block's largest stay normal fp16 numbers (11
+// significant bits).  e goes to vexp[g * nblk + b]; the attention kernels fold
+// it into P (see vexp_next in bt_common.h).  Layout: block b of head g at vt +
+// (g * nblk + b) * 64 * D as 8 key chunks; chunk c holds at row d the 8
+// values V[b*64 + key][d] (16 bytes) of
 //   order kVtOrder16: key = (c/4)*32 + (c%4)*4 + {0, 1, 2, 3, 16, 17, 18, 19},
 //     the order in which lane group c%4 of a 16x16 MFMA result holds P of the
 //     32-key half c/4;
 //   order kVtOrder32: key = (c/2)*16 + (c%2)*4 + {0, 1, 2, 3, 8, 9, 10, 11},
 //     the order in which a 32x32 MFMA result's registers hold P of the 16-key
 //     step c/2 for lane half c%2.
-// Keys past kv_len are zero.  One thread per (chunk, 8-column slice)
-// transposes an 8 x 8 tile in registers; the block's image is assembled in
-// LDS and stored linearly (1 KiB per wave instruction): 16-byte unit x sits in
-// LDS slot x ^ ((x >> 3) & 7), conflict-free both ways.
+// One thread per (chunk, 8-column slice) transposes an 8 x 8 tile in
+// registers; the block's image is assembled in LDS and stored linearly (1 KiB
+// per wave instruction): 16-byte unit x sits in LDS slot x ^ ((x >> 3) & 7),
+// conflict-free both ways.
+//
+// K image, block b of kv head g: e = E - 14 for the block's largest |k| (0 for
+// a block of zeros), the image holds k * 2^-e in [2^14, 2^15) at most, and e
+// goes to kexp[g * nblk + b]; the kernels multiply the scores of the block by
+// 2^e (with q's own per-row scale) in the softmax's exp2 argument, which is
+// exact.  Layout: row-major, block b of head g at kimg + (g * nblk + b) * 64 *
+// D; the 16-byte slot s of row r holds the 8 values of chunk s ^ (r & 15)
+// (columns 8 * (s ^ (r & 15)) ..), the XOR swizzle the kernels' K tiles use in
+// LDS, so a tile copy is a plain contiguous copy.
+//
+// Keys past kv_len are zero in both images.
 #include "bt_common.h"
 #include "bt_kernels.h"
 
@@ -35,6 +46,7 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
   constexpr int kDC = D / 8;                 // 16-byte column chunks per row
   constexpr int kItems = 8 * kDC;            // (chunk, column chunk) items per block
   static_assert(kItems <= 256, "one item per thread");
+  static_assert(kPrefillKeyBlock * kDC % 256 == 0, "whole K units per thread");
   constexpr int kBlk = kPrefillKeyBlock;
   const int blk = blockIdx.x, g = blockIdx.y;
   const int nblk = gridDim.x;
@@ -45,9 +57,26 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
   uint16_t* img = p.vt + ((size_t)g * nblk + blk) * kBlk * D;
   constexpr int kUnits = kBlk * D * 2 / 16;
   __shared__ __attribute__((aligned(16))) u32x4 stage[kUnits];
-  __shared__ uint32_t wmax[4];
+  __shared__ uint32_t wmax[2][4];
   const int item = threadIdx.x;
   const int c = item / kDC, dc = item % kDC;
+  // K: unit x = j * 256 + thread is slot x % kDC of row x / kDC; it holds
+  // source chunk slot ^ (row & 15).
+  constexpr int kKUnits = kBlk * kDC / 256;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.k + (int64_t)g * p.kv_stride_head), (short)0,
+      (int)((uint32_t)(p.q_offset + p.seqlen) * row_bytes), 0x00020000);
+  u32x4 krow[kKUnits];
+  uint32_t kmx = 0;  // largest |k| as bf16 bits
+#pragma unroll
+  for (int j = 0; j < kKUnits; ++j) {
+    const int x = j * 256 + item;
+    const int r = x / kDC, slot = x % kDC;
+    krow[j] = __builtin_amdgcn_raw_buffer_load_b128(
+        krs, (int)((uint32_t)(blk * kBlk + r) * row_bytes + (uint32_t)(slot ^ (r & 15)) * 16), 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kmx = max(kmx, max(krow[j][i] & 0x7fffu, (krow[j][i] >> 16) & 0x7fffu));
+  }
   u32x4 rows[8];
   uint32_t mx = 0;  // largest |v| as bf16 bits (monotonic in |v|)
   if (item < kItems) {
@@ -61,10 +90,35 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
     }
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  for (int o = 32; o > 0; o >>= 1) {
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+    kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, o, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    wmax[0][threadIdx.x >> 6] = mx;
+    wmax[1][threadIdx.x >> 6] = kmx;
+  }
   __syncthreads();
-  mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  mx = max(max(wmax[0][0], wmax[0][1]), max(wmax[0][2], wmax[0][3]));
+  kmx = max(max(wmax[1][0], wmax[1][1]), max(wmax[1][2], wmax[1][3]));
+  int ek = 0;
+  if (kmx != 0) {
+    const int ebits = (int)(kmx >> 7);
+    ek = (ebits == 0 ? 1 : ebits) - 127 - 14;
+  }
+  if (threadIdx.x == 0) p.kexp[g * nblk + blk] = ek;
+  uint16_t* kimg = p.kimg + ((size_t)g * nblk + blk) * kBlk * D;
+#pragma unroll
+  for (int j = 0; j < kKUnits; ++j) {
+    u32x4 o;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float f0 = __uint_as_float(krow[j][m] << 16), f1 = __uint_as_float(krow[j][m] & 0xffff0000u);
+      o[m] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                              (float2_v){__builtin_ldexpf(f0, -ek), __builtin_ldexpf(f1, -ek)}, half2_v));
+    }
+    reinterpret_cast<u32x4*>(kimg)[j * 256 + item] = o;
+  }
   int e = kVExpZero;
   if (mx != 0) {
     const int ebits = (int)(mx >> 7);                 // biased exponent (0: subnormal)

@@ -146,9 +146,9 @@ int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, c
                          void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
                          int64_t out_stride_seq, void* stream);
 
-/* Bytes of prefill workspace (the transposed fp16 V image the prefill builds
- * once per call, with one power-of-two scale per 64-key block) for kv_len =
- * q_offset + seqlen keys; 0 for invalid arguments.  Like
+/* Bytes of prefill workspace (the fp16 K image and transposed fp16 V image
+ * the prefill builds once per call, each with one power-of-two scale per
+ * 64-key block) for kv_len = q_offset + seqlen keys; 0 for invalid arguments.  Like
  * bt_decode_workspace_bytes it replaces a per-call allocation: the
  * reference's SDPA call (prefill.py:60-68) allocates its scratch internally. */
 int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t head_dim);
@@ -164,14 +164,14 @@ int64_t bt_prefill_workspace_bytes(int32_t kv_len, int32_t kv_heads, int32_t hea
 int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32_t heads,
                                          int32_t kv_heads, int32_t head_dim);
 
-/* Causal GQA prefill attention on bf16 MFMA.  Replaces the
+/* Causal GQA prefill attention on fp16 MFMA.  Replaces the
  * F.scaled_dot_product_attention(is_causal=True, enable_gqa=True) call of
  * _prefill_attn (breezetoken/model/prefill.py:56-68; q_offset = 0) and the
  * banded-mask chunked prefill of Qwen36MoE._attn_batch
  * (breezetoken/model/qwen36_moe.py:394-428; q_offset = pos0).  q (seqlen,
  * heads, D): the new tokens, at absolute positions q_offset .. q_offset +
- * seqlen - 1, f32 (as the reference computes it, prefill.py:49-68; Q.K^T then
- * uses its bf16 high and low parts; group sizes 1, 2, 4, 8) or bf16 (q_dtype);
+ * seqlen - 1, f32 (as the reference computes it, prefill.py:49-68) or bf16
+ * (q_dtype); Q.K^T takes q as fp16 scaled by a power of two per row;
  * k/v (q_offset + seqlen, kv_heads, D) bf16 with the given strides
  * (token-major or head-major caches both fit): the cache including the new
  * tokens.  Query row i attends keys 0 .. q_offset + i.  out (seqlen, heads, D)

@@ -56,10 +56,11 @@ def test_workspace_bytes():
     assert lib.bt_decode_workspace_bytes(8, 256, 128) == 4096 + 8 * 128 * 256 * 4
     assert lib.bt_decode_workspace_bytes(8, 256, 1) == 256 + 8 * 256 * 4
     assert lib.bt_decode_workspace_bytes(0, 256, 1) == 0
-    # prefill: one fp16 V^T image per kv head, whole 64-key blocks, then one
-    # int32 scale exponent per kv head and block (256-byte aligned)
-    assert lib.bt_prefill_workspace_bytes(8192, 2, 256) == 2 * 8192 * 256 * 2 + 1024
-    assert lib.bt_prefill_workspace_bytes(65, 1, 128) == 128 * 128 * 2 + 256
+    # prefill: the fp16 V^T image (one per kv head, whole 64-key blocks), one
+    # int32 scale exponent per kv head and block, then the fp16 K image and its
+    # exponents (each part 256-byte aligned)
+    assert lib.bt_prefill_workspace_bytes(8192, 2, 256) == 2 * (2 * 8192 * 256 * 2 + 1024)
+    assert lib.bt_prefill_workspace_bytes(65, 1, 128) == 2 * (128 * 128 * 2 + 256)
     assert lib.bt_prefill_workspace_bytes(0, 1, 128) == 0
     # the split-key size refuses the same malformed shapes (before any device query)
     assert lib.bt_prefill_split_workspace_bytes(0, 0, 8, 2, 256) == 0
@@ -268,7 +269,7 @@ def test_gemv_refuses_bad_arguments_and_sizes_its_workspace():
 )
 def test_prefill_split_plan_sizes(steps, q_offset, heads, max_chunks):
     """The split-key plan on a 256-CU device (the count assumed without a GPU):
-    the workspace is the V^T image and its block scales plus f32 partials and
+    the workspace is the V^T and K images and their block scales plus f32 partials and
     LSEs of kv_heads x query blocks x max_chunks x 128 rows.  S = 8192 runs the
     pair kernel, which needs no partials."""
     from breezetoken_amd import _lib
@@ -277,7 +278,7 @@ def test_prefill_split_plan_sizes(steps, q_offset, heads, max_chunks):
     kv, dim = 2, 256
     vt = lib.bt_prefill_workspace_bytes(q_offset + steps, kv, dim)
     nblk = -(-(q_offset + steps) // 64)
-    assert vt == kv * nblk * 64 * dim * 2 + -(-(kv * nblk * 4) // 256) * 256
+    assert vt == 2 * (kv * nblk * 64 * dim * 2 + -(-(kv * nblk * 4) // 256) * 256)
     got = lib.bt_prefill_split_workspace_bytes(steps, q_offset, heads, kv, dim)
     if max_chunks == 0:
         assert got == vt

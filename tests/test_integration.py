@@ -139,8 +139,9 @@ def test_prefill_predicate_and_fallback():
     assert "not served" in bk.prefill_unserved(q, k, v, 0)
     q3 = torch.randn(S, 6, 128, generator=g)
     k3 = torch.randn(S, 2, 128, generator=g).to(torch.bfloat16)
-    assert "group sizes 1, 2, 4 and 8" in bk.prefill_unserved(q3, k3, k3.clone(), 0)
+    assert "GPU" in bk.prefill_unserved(q3, k3, k3.clone(), 0)
     assert "GPU" in bk.prefill_unserved(q3.to(torch.bfloat16), k3, k3.clone(), 0)
+    assert "f32 or bf16 q" in bk.prefill_unserved(q3.half(), k3, k3.clone(), 0)
     be = _CpuBackend()
     qq, kk, vv = q.transpose(0, 1).unsqueeze(0), k.transpose(0, 1).unsqueeze(0), v.transpose(0, 1).unsqueeze(0)
     got = be.prefill_sdpa(qq, kk, vv, D ** -0.5)

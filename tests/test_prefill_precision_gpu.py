@@ -3,9 +3,9 @@ any bf16 magnitude.
 
 * The reference keeps q in f32 through RMSNorm/RoPE into SDPA
   (breezetoken/model/prefill.py:49-68).  bt_gqa_prefill takes that f32 q
-  (carried as a bf16 hi/lo pair through Q.K^T) and is held to the parity gate
-  (max-abs 2e-3, cosine 0.99999) against the oracle's f32 SDPA on the same
-  unrounded q.
+  (rounded to fp16 after a power-of-two scale per row for Q.K^T: 11
+  significant bits against bf16's 8) and is held to the parity gate (max-abs
+  2e-3, cosine 0.99999) against the oracle's f32 SDPA on the same unrounded q.
 * V enters P.V as fp16 scaled by a power of two per 64-key block, so bf16 V
   beyond fp16's range (|v| > 65504) or deep in its subnormals (|v| ~ 1e-5 and
   below) must still match.  Each prefill kernel path is run on V patterns with
@@ -45,8 +45,19 @@ def test_c4_prefill_f32_q_matches_reference_arithmetic(hip_backend, steps):
     assert err <= ATOL and cos >= COS
 
 
+def test_c4_prefill_8192_f32_q_sampled_rows(hip_backend):
+    """The benchmark shape with f32 q: sampled rows against decode attention
+    over keys 0..i in f32."""
+    q, k, v, scale = wl.c4_inputs(8192, q_f32=True)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu()
+    for i in [0, 1, 31, 32, 63, 64, 1000, 4095, 4096, 8000, 8190, 8191]:
+        ref = orc.torch_attention(q[i], k[: i + 1].float(), v[: i + 1].float(), scale)
+        err, cos = orc.compare(out[i].numpy(), ref.numpy())
+        assert err <= ATOL and cos >= COS, (i, err, cos)
+
+
 def test_c4_prefill_f32_q_error_below_bf16_q(hip_backend):
-    """Carrying q as hi/lo must beat rounding it to bf16 (the error it removes)."""
+    """Taking q as scaled fp16 must beat rounding it to bf16 (which alone misses the gate)."""
     q, k, v, scale = wl.c4_inputs(512, q_f32=True)
     ref = orc.torch_prefill_attention(q, k.float(), v.float(), scale).numpy()
     e32, _ = orc.compare(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu().numpy(), ref)
@@ -79,13 +90,14 @@ def _v_pattern(name: str, kv_len: int, kv: int, dim: int, g: torch.Generator) ->
 V_PATTERNS = ["uniform_3e4", "uniform_1e5", "uniform_1e-5", "uniform_1e-30", "outlier_rows_1e5",
               "alternating_blocks", "zero_blocks", "big_then_tiny", "tiny_then_big"]
 # (name, heads, kv, dim, steps, q_offset, q dtype, split_keys): the pair kernel
-# (f32 q), the two-waves-per-SIMD kernel alone and with split keys (bf16 q,
-# short prompt), the one-wave kernel (group size 3).
+# (its grid fills 256 CUs: 16 kv heads x 1024 / 64 query-block pairs), the
+# two-waves-per-SIMD kernel alone and with split keys (short prompts), the
+# one-wave kernel (group size 3).
 PATHS = [
-    ("pair_f32q", 8, 2, 256, 320, 0, torch.float32, True),
-    ("prefill8", 8, 2, 256, 320, 0, torch.bfloat16, False),
-    ("prefill8_split", 8, 2, 128, 96, 640, torch.bfloat16, True),
-    ("onewave_g3", 6, 2, 128, 200, 0, torch.bfloat16, True),
+    ("pair_f32q", 64, 16, 128, 1024, 0, torch.float32, True),
+    ("prefill8_f32q", 8, 2, 256, 320, 0, torch.float32, False),
+    ("prefill8_split_bf16q", 8, 2, 128, 96, 640, torch.bfloat16, True),
+    ("onewave_g3_f32q", 6, 2, 128, 200, 0, torch.float32, True),
 ]
 
 
