@@ -111,12 +111,93 @@ def pmc_mode(torch, backend, dev) -> int:
     return 0
 
 
-def prefill_mode(torch, backend, dev, calls: int) -> int:
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's description."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.lower().startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or platform.machine()
+
+
+def time_cpu(fn, seconds: float, min_calls: int = 20, max_calls: int = 2000) -> tuple[float, int]:
+    """Median seconds per call of ``fn`` after 3 warm-up calls: at least
+    ``min_calls`` calls, more while ``seconds`` last."""
+    for _ in range(3):
+        fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_calls or (time.perf_counter() < t_end and len(times) < max_calls):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baselines(torch, head_case, L: int, nbytes: int, seconds: float, headline_only: bool):
+    """The reference's torch f32 CPU attention (restated in oracle/, as the
+    reference computes it: backends.py:196-215 for decode, prefill.py:56-68 for
+    prefill) on the host cores: the config-2 headline row, then one row per
+    further config (C3 at 32k, C4 causal prefill, C5 looping over its 32
+    sequences).  Returns (headline dict, rows)."""
+    from breezetoken_amd import workloads as wl
+    from oracle.attention import torch_attention, torch_prefill_attention
+
+    threads = torch.get_num_threads()
+    host = f"cpu={os.cpu_count()} logical ({cpu_model()}), torch threads={threads}"
+    qc, kc, vc = head_case.q.float(), head_case.k[:L].float(), head_case.v[:L].float()
+    med, n = time_cpu(lambda: torch_attention(qc, kc, vc, head_case.scale), seconds)
+    head = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_call": round(med * 1e6, 1), "cpu_model": cpu_model(),
+            "sample": f"{n} calls of config-2 decode (valid 32768, H=8, Hkv=2, D=256) in torch f32 SDPA "
+                      f"on the host CPU, median after 3 warm-ups; {host}"}
+    log(f"cpu baseline: {med * 1e6:.0f} us/call on {threads} threads ({cpu_model()})")
+    rows = []
+    if headline_only:
+        return head, rows
+    c3 = wl.c3_inputs(32768)
+    q3, k3, v3 = c3.q.float(), c3.k.float(), c3.v.float()
+    med, n = time_cpu(lambda: torch_attention(q3, k3, v3, c3.scale), seconds / 3)
+    b3 = wl.decode_bytes(32768, 16, 2, 256)
+    rows.append({"config": "C3 decode, H=16 Hkv=2 D=256, valid 32768", "us_per_call": round(med * 1e6, 1),
+                 "GBps": round(b3 / med / 1e9, 3), "calls": n})
+    for steps, min_calls in ((512, 20), (2048, 20), (8192, 3)):
+        q4, k4, v4, sc4 = wl.c4_inputs(steps)
+        q4, k4, v4 = q4.float(), k4.float(), v4.float()
+        med, n = time_cpu(lambda: torch_prefill_attention(q4, k4, v4, sc4), seconds / 3, min_calls=min_calls)
+        fl = wl.prefill_flops(steps, 8, 256)
+        rows.append({"config": f"C4 causal prefill, H=8 Hkv=2 D=256, S={steps}", "us_per_call": round(med * 1e6, 1),
+                     "TFLOPs": round(fl / med / 1e12, 4), "calls": n})
+    c5 = wl.c5_inputs()
+    seqs = [(c5.q[b].float(), c5.k[o:o + n_].float(), c5.v[o:o + n_].float())
+            for b, (o, n_) in enumerate(zip(c5.offsets, c5.lens))]
+
+    def c5_loop():
+        for qq, kk, vv in seqs:
+            torch_attention(qq, kk, vv, c5.scale)
+
+    med, n = time_cpu(c5_loop, seconds / 3)
+    b5 = 2 * sum(c5.lens) * 2 * 256 * 2 + len(c5.lens) * 8 * 256 * 4 * 2
+    rows.append({"config": "C5 ragged decode, 32 sequences looped, H=8 Hkv=2 D=256", "us_per_call": round(med * 1e6, 1),
+                 "GBps": round(b5 / med / 1e9, 3), "calls": n})
+    for r in rows:
+        r["host"] = host
+    log("cpu rows: " + json.dumps(rows))
+    return head, rows
+
+
+def prefill_mode(torch, backend, dev, calls: int, q_f32: bool = False) -> int:
     """Config-4 prefill at S=8192 only (for rocprofv3 kernel traces): ``calls``
-    calls after two warm-up calls, timed with HIP events on the current stream."""
+    calls after two warm-up calls, timed with HIP events on the current stream.
+    q is bf16 as config 4 draws it, or its f32 draws (``q_f32``)."""
     from breezetoken_amd import workloads as wl
 
-    q, k, v, scale = wl.c4_inputs(8192)
+    q, k, v, scale = wl.c4_inputs(8192, q_f32=q_f32)
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
     for _ in range(2):
         backend.attention_prefill(q, k, v, scale, torch.bfloat16)
@@ -129,7 +210,8 @@ def prefill_mode(torch, backend, dev, calls: int) -> int:
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1e3 / calls
     fl = wl.prefill_flops(8192, 8, 256)
-    print(json.dumps({"mode": "prefill", "steps": 8192, "calls": calls, "us_per_call": round(us, 2),
+    print(json.dumps({"mode": "prefill", "steps": 8192, "q_dtype": "f32" if q_f32 else "bf16", "calls": calls,
+                      "us_per_call": round(us, 2),
                       "TFLOPs": round(fl / us / 1e6, 1)}), flush=True)
     return 0
 
@@ -205,6 +287,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--q-f32", action="store_true", help="prefill mode: f32 q (the reference's prefill arithmetic)")
     ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "ragged", "chunked"], default="bench",
                     help="pmc: only a 256 MiB device copy and the config-2 split kernel, "
                          "5 launches each, for rocprofv3 --pmc runs; prefill: only config-4 "
@@ -235,7 +318,7 @@ def main() -> int:
     if args.mode == "pmc":
         return pmc_mode(torch, backend, dev)
     if args.mode == "prefill":
-        return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)))
+        return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)), args.q_f32)
     if args.mode == "ragged":
         return ragged_mode(torch, backend, dev, max(1, min(args.steps, 500)))
     if args.mode == "chunked":
@@ -354,10 +437,11 @@ def main() -> int:
         log(f"c5 ragged: {rms * 1e3:.2f} us/call")
         del rkv
         torch.cuda.empty_cache()
-        # prefill (config 4), if served
+        # prefill (config 4: bf16 q/k/v, bf16 output), and at S = 8192 also with the
+        # same q draws in f32, as the reference's prefill computes it (prefill.py:49-68)
         pre = []
-        for s in (128, 512, 2048, 8192):
-            qp, kp, vp, sc = (t.to(dev) if hasattr(t, "to") else t for t in wl.c4_inputs(s))
+        for s, qf32 in ((128, False), (512, False), (2048, False), (8192, False), (8192, True)):
+            qp, kp, vp, sc = (t.to(dev) if hasattr(t, "to") else t for t in wl.c4_inputs(s, q_f32=qf32))
             try:
                 pms = time_graph(torch, lambda: backend.attention_prefill(qp, kp, vp, sc, torch.bfloat16),
                                  max(20, esteps // 10), 5)
@@ -365,16 +449,17 @@ def main() -> int:
                 pre.append({"steps": s, "error": str(exc)[:120]})
                 break
             fl = wl.prefill_flops(s, 8, 256)
-            pre.append({"steps": s, "us_per_call": pms * 1e3, "TFLOPs": fl / (pms * 1e-3) / 1e12,
+            pre.append({"steps": s, "q_dtype": "f32" if qf32 else "bf16", "us_per_call": pms * 1e3,
+                        "TFLOPs": fl / (pms * 1e-3) / 1e12,
                         "frac_bf16_peak": fl / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS})
         extra["c4_prefill"] = pre
-        if pre and "TFLOPs" in pre[-1]:
-            big = pre[-1]
-            # the call = V^T pre-pass + MFMA kernel; both inside the timed region
+        big = next((r for r in pre if r.get("steps") == 8192 and r.get("q_dtype") == "bf16" and "TFLOPs" in r), None)
+        if big:
+            # the call = K/V^T image pre-pass + MFMA kernel; both inside the timed region
             extra["c4_prefill_roofline"] = {
                 "bound": "mfma", "achieved": round(big["TFLOPs"], 1), "peak": BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(big["frac_bf16_peak"], 4), "steps": big["steps"],
-                "kernels": "prefill_vt8_kernel<256> + gqa_prefill8_kernel<256>",
+                "kernels": "prefill_vts_kernel<256,0> + gqa_prefill_pair_kernel<256>",
                 "algorithmic_flops": wl.prefill_flops(big["steps"], 8, 256)}
         log("c4: " + json.dumps(pre))
         # chunked prefill at a cached prefix (qwen36_moe.py:394-428) and a short prompt:
@@ -503,27 +588,9 @@ def main() -> int:
     # ------------------------------------------------------------ CPU baseline
     cpu_baseline = None
     if not args.no_cpu:
-        from oracle.attention import torch_attention  # the reference CPU path, restated
-
-        threads = torch.get_num_threads()
-        qc = head_case.q.float()
-        kc = head_case.k[:L].float()
-        vc = head_case.v[:L].float()
-        for _ in range(3):
-            torch_attention(qc, kc, vc, head_case.scale)
-        times = []
-        t_end = time.perf_counter() + args.cpu_seconds
-        while len(times) < 20 or (time.perf_counter() < t_end and len(times) < 2000):
-            t0 = time.perf_counter()
-            torch_attention(qc, kc, vc, head_case.scale)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        cpu_baseline = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-                        "kind": "port", "us_per_call": round(med * 1e6, 1),
-                        "sample": f"{len(times)} calls of config-2 decode (valid 32768, H=8, Hkv=2, "
-                                  f"D=256) in torch f32 SDPA on the host CPU, median; "
-                                  f"cpu={os.cpu_count()} logical, torch threads={threads}"}
-        log(f"cpu baseline: {med * 1e6:.0f} us/call on {threads} threads")
+        cpu_baseline, cpu_rows = cpu_baselines(torch, head_case, L, nbytes, args.cpu_seconds, args.no_extra)
+        if cpu_rows:
+            extra["cpu_rows"] = cpu_rows
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,

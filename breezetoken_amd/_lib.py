@@ -55,6 +55,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i32,
         [_vp, _c_i32, _c_i32, _vp, _c_i32, _vp, _vp, _vp],
     ),
+    "bt_ragged_plan_device": (
+        ctypes.c_int,
+        [_vp, _c_i32, _c_i32, _vp, _c_i32, _vp, _vp, _vp, _vp],
+    ),
     "bt_gqa_decode_ragged": (
         ctypes.c_int,
         [_vp, _c_i32, _c_i64, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32,

@@ -39,6 +39,7 @@ backends.py:698 with graph.py:127-133).
 from __future__ import annotations
 
 import ctypes
+from collections import OrderedDict
 
 import torch
 
@@ -163,28 +164,43 @@ class HipBackend:
         props = torch.cuda.get_device_properties(dev)
         self.num_cus = int(props.multi_processor_count)
         self.arch = getattr(props, "gcnArchName", "")
-        self._ws: dict[tuple, torch.Tensor] = {}
-        self._plans: dict[tuple, tuple] = {}
+        self._ws: dict[tuple | str, torch.Tensor] = {}
+        # Buffers a captured graph may still point at after a larger one
+        # replaced them: kept until close().
+        self._retired: list[torch.Tensor] = []
+        self._plans: "OrderedDict[tuple, tuple]" = OrderedDict()
+        self._pinned_plans: dict[tuple, tuple] = {}
+        self._dev_plans: dict[tuple, tuple] = {}
 
     # ------------------------------------------------------------------ utils
-    def _workspace(self, heads: int, dim: int, total_splits: int) -> torch.Tensor:
-        key = (heads, dim, total_splits)
+    def _grow(self, key, nbytes: int) -> torch.Tensor:
+        """A workspace of at least ``nbytes`` under ``key``.  It only grows; a
+        replaced buffer is retired, not freed, because a captured graph may
+        still point at it (everything is released by close())."""
         ws = self._ws.get(key)
-        if ws is None:
-            nbytes = int(self._lib.bt_decode_workspace_bytes(heads, dim, total_splits))
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=self._dev)
-            self._ws[key] = ws  # kept until close(): captured graphs may point at it
+        if ws is None or ws.numel() < nbytes:
+            if ws is not None:
+                self._retired.append(ws)
+            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self._dev)
+            self._ws[key] = ws
         return ws
 
+    def _workspace(self, heads: int, dim: int, total_splits: int) -> torch.Tensor:
+        """Decode partials for ``total_splits`` splits of (heads, dim): one
+        buffer per (heads, dim), sized at first use for at least the largest
+        single-sequence split count."""
+        want = max(total_splits, self._max_splits())
+        nbytes = int(self._lib.bt_decode_workspace_bytes(heads, dim, want))
+        return self._grow(("decode", heads, dim), nbytes)
+
+    def _max_splits(self) -> int:
+        return int(self._lib.bt_decode_pick_splits(1, 1 << 30, self.num_cus))
+
     def _prefill_workspace(self, steps: int, q_offset: int, heads: int, kv_heads: int, dim: int) -> torch.Tensor:
-        """Room for the V^T image and, where the library splits the key range
-        (short prompts, long cached prefixes), its partials."""
+        """Room for the K and V^T images and, where the library splits the key
+        range (short prompts, long cached prefixes), its partials."""
         nbytes = int(self._lib.bt_prefill_split_workspace_bytes(steps, q_offset, heads, kv_heads, dim))
-        ws = self._ws.get("prefill")
-        if ws is None or ws.numel() < nbytes:
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=self._dev)
-            self._ws["prefill"] = ws  # grows only; kept until close()
-        return ws
+        return self._grow("prefill", nbytes)
 
     @property
     def tile_tokens(self) -> int:
@@ -332,19 +348,38 @@ class HipBackend:
         return out
 
     # ----------------------------------------------------------- ragged decode
+    MAX_HOST_PLANS = 64
+
     def ragged_plan(self, lens: list[int], kv_heads: int, target_groups: int | None = None):
-        """Split plan for a ragged batch, as device tables (cached): sequence b gets
-        ceil(len_b / T) splits for the smallest token cap T whose total fits
-        ``target_groups`` work-groups per kv head (default: one round, CUs / kv heads)."""
+        """Split plan for a ragged batch from host lengths, as device tables:
+        sequence b gets ceil(len_b / T) splits for the smallest token cap T
+        whose total fits ``target_groups`` work-groups per kv head (default:
+        one round, CUs / kv heads).  Plans are cached per (lens, target), at
+        most MAX_HOST_PLANS of them (least recently used first out); a plan
+        used while a graph is being captured is kept until close()."""
         if target_groups is None:
             target_groups = max(1, self.num_cus // max(1, kv_heads))
         key = (tuple(int(x) for x in lens), int(target_groups))
-        plan = self._plans.get(key)
-        if plan is not None:
-            return plan
+        plan = self._pinned_plans.get(key)
+        if plan is None:
+            plan = self._plans.get(key)
+            if plan is not None:
+                self._plans.move_to_end(key)
+        if plan is None:
+            plan = self._host_plan(key)
+            self._plans[key] = plan
+            while len(self._plans) > self.MAX_HOST_PLANS:
+                self._plans.popitem(last=False)
+        if torch.cuda.is_current_stream_capturing() and key not in self._pinned_plans:
+            self._pinned_plans[key] = plan
+            self._plans.pop(key, None)
+        return plan
+
+    def _host_plan(self, key):
+        lens, target_groups = key
         batch = len(lens)
         cap = sum(max(1, -(-int(x) // 32)) for x in lens)
-        lens_c = (ctypes.c_int32 * batch)(*[int(x) for x in lens])
+        lens_c = (ctypes.c_int32 * batch)(*lens)
         work = (ctypes.c_int32 * (4 * cap))()
         base = (ctypes.c_int32 * batch)()
         count = (ctypes.c_int32 * batch)()
@@ -359,25 +394,58 @@ class HipBackend:
         work_t = torch.tensor(list(work)[: 4 * n], dtype=torch.int32).to(dev)
         base_t = torch.tensor(list(base), dtype=torch.int32).to(dev)
         count_t = torch.tensor(list(count), dtype=torch.int32).to(dev)
-        plan = (work_t, n, base_t, count_t, int(total.value))
-        self._plans[key] = plan
-        return plan
+        return (work_t, n, base_t, count_t, int(total.value))
+
+    def ragged_plan_device(self, seq_len: torch.Tensor, target_groups: int | None = None):
+        """The same plan built on the device from the device lengths ``seq_len``
+        (B,) int32, on the current stream with no host synchronisation
+        (capturable).  Tables are allocated once per (B, target) and kept until
+        close(); returns (work, num_work, split_base, split_count, total_splits)
+        with num_work = total_splits = the table capacity max(B, target)."""
+        batch = int(seq_len.numel())
+        if target_groups is None:
+            raise ValueError("target_groups is required (CUs / kv heads for one round)")
+        cap = max(batch, int(target_groups))
+        key = (batch, int(target_groups))
+        bufs = self._dev_plans.get(key)
+        if bufs is None:
+            bufs = (torch.empty((cap, 4), dtype=torch.int32, device=self._dev),
+                    torch.empty(batch, dtype=torch.int32, device=self._dev),
+                    torch.empty(batch, dtype=torch.int32, device=self._dev),
+                    torch.empty(1, dtype=torch.int32, device=self._dev))
+            self._dev_plans[key] = bufs
+        work, base, count, total = bufs
+        if seq_len.dtype != torch.int32 or seq_len.device != self._dev or not seq_len.is_contiguous():
+            raise RuntimeError("seq_len must be a contiguous int32 device tensor")
+        rc = self._lib.bt_ragged_plan_device(
+            seq_len.data_ptr(), batch, int(target_groups), work.data_ptr(), cap, base.data_ptr(),
+            count.data_ptr(), total.data_ptr(), _stream(self._dev),
+        )
+        check("bt_ragged_plan_device", rc)
+        return work, cap, base, count, cap
 
     def attention_ragged(
         self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_offset: torch.Tensor,
-        seq_len: torch.Tensor, lens: list[int], scale: float, target_groups: int | None = None,
+        seq_len: torch.Tensor, lens: list[int] | None, scale: float, target_groups: int | None = None,
     ) -> torch.Tensor:
         """Ragged decode: sequence b reads slots [seq_offset[b], seq_offset[b] + seq_len[b]).
 
-        q (B, H, D); seq_offset (B,) int64 and seq_len (B,) int32 on the device;
-        ``lens`` the same lengths on the host, used only to plan split counts.
+        q (B, H, D); seq_offset (B,) int64 and seq_len (B,) int32 on the device.
+        ``lens``: the same lengths on the host, used to plan split counts there;
+        None plans on the device from ``seq_len`` instead (no host round trip,
+        so a decode step over growing sequences can be captured in a graph).
         """
         batch, heads, dim = q.shape
         groups = self._check_kv(k, v, heads, dim)
         if seq_offset.dtype != torch.int64 or seq_len.dtype != torch.int32:
             raise RuntimeError("seq_offset must be int64 and seq_len int32")
         q = q.contiguous()
-        work, n, base, count, total = self.ragged_plan(lens, groups, target_groups)
+        if target_groups is None:
+            target_groups = max(1, self.num_cus // max(1, groups))
+        if lens is None:
+            work, n, base, count, total = self.ragged_plan_device(seq_len, target_groups)
+        else:
+            work, n, base, count, total = self.ragged_plan(lens, groups, target_groups)
         ws = self._workspace(heads, dim, total)
         out = torch.empty((batch, heads, dim), dtype=torch.float32, device=self._dev)
         rc = self._lib.bt_gqa_decode_ragged(
@@ -627,7 +695,10 @@ class HipBackend:
 
     def close(self) -> None:
         self._ws.clear()
+        self._retired.clear()
         self._plans.clear()
+        self._pinned_plans.clear()
+        self._dev_plans.clear()
 
     def __repr__(self) -> str:
         return f"HipBackend(device={self.device!r}, arch={self.arch!r}, cus={self.num_cus})"

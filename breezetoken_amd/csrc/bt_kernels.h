@@ -208,6 +208,21 @@ inline int decode_mode(bool work, bool pos, bool seq_len, bool seq_offset, int b
   return (batch == 1 && !seq_offset) ? 0 : -1;
 }
 
+// Device-side ragged plan (ragged_plan.hip): the plan bt_ragged_plan makes on
+// the host, from device lengths, padded to work_capacity entries with {-1, ..}.
+constexpr int kRaggedPlanMaxBatch = 4096;
+struct RaggedPlanParams {
+  const int32_t* seq_len;  // (batch,) device lengths
+  int32_t batch;
+  int32_t target_groups;
+  int32_t* work;           // (work_capacity, 4) entries {b, s, ns_b, base_b}
+  int32_t work_capacity;   // >= max(batch, target_groups)
+  int32_t* split_base;     // (batch,)
+  int32_t* split_count;    // (batch,)
+  int32_t* total;          // optional: the number of real entries
+};
+hipError_t launch_ragged_plan(const RaggedPlanParams& p, hipStream_t stream);
+
 hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int grid_x, int batch,
                                hipStream_t stream);
 hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads, int batch,

@@ -383,6 +383,25 @@ int32_t bt_ragged_plan(const int32_t* lens, int32_t batch, int32_t target_groups
   return total;
 }
 
+int bt_ragged_plan_device(const int32_t* seq_len, int32_t batch, int32_t target_groups, int32_t* work,
+                          int32_t work_capacity, int32_t* split_base, int32_t* split_count,
+                          int32_t* total_splits, void* stream) {
+  if (!seq_len || !work || !split_base || !split_count) return BT_EINVAL;
+  if (batch < 1 || target_groups < 1 || !aligned16(work)) return BT_EINVAL;
+  if (batch > bt::kRaggedPlanMaxBatch) return BT_ENOTSUP;
+  if (work_capacity < std::max(batch, target_groups)) return BT_ENOSPC;
+  bt::RaggedPlanParams p{};
+  p.seq_len = seq_len;
+  p.batch = batch;
+  p.target_groups = target_groups;
+  p.work = work;
+  p.work_capacity = work_capacity;
+  p.split_base = split_base;
+  p.split_count = split_count;
+  p.total = total_splits;
+  return hip_rc(bt::launch_ragged_plan(p, (hipStream_t)stream));
+}
+
 int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,
                          const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
                          const int64_t* seq_offset, const int32_t* seq_len, int32_t batch,

@@ -150,6 +150,7 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   if constexpr (MODE == kModeRagged) {
     const int* w = reinterpret_cast<const int*>(p.work) + 4 * (int)blockIdx.x;
     b = uniform_load(w, 0); s = uniform_load(w, 1); ns = uniform_load(w, 2); base = uniform_load(w, 3);
+    if (b < 0) return;  // padding entry of a device-built plan
   } else {
     b = blockIdx.z; s = blockIdx.x; ns = p.num_split; base = b * p.num_split;
   }

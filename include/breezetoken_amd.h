@@ -132,9 +132,26 @@ int32_t bt_ragged_plan(const int32_t* lens, int32_t batch, int32_t target_groups
                        int32_t* work, int32_t work_capacity, int32_t* split_base,
                        int32_t* split_count, int32_t* total_splits);
 
+/* Device-side planner for ragged batches: the plan bt_ragged_plan makes, built
+ * on `stream` from the device lengths seq_len[batch] (negative lengths count
+ * as 0), so a decode step over many growing sequences needs no host
+ * synchronisation and can be captured in a graph.  work (16-byte aligned,
+ * work_capacity >= max(batch, target_groups) entries of 4 int32) gets the
+ * real entries followed by padding entries {-1, 0, 0, 0} up to its capacity;
+ * split_base/split_count as bt_ragged_plan; *total_splits (device, optional)
+ * the number of real entries.  Pass work_capacity as both num_work and
+ * total_splits to bt_gqa_decode_ragged, whose split kernel skips the padding.
+ * batch <= 4096.  No reference counterpart (the reference decodes one
+ * sequence). */
+int bt_ragged_plan_device(const int32_t* seq_len, int32_t batch, int32_t target_groups,
+                          int32_t* work, int32_t work_capacity, int32_t* split_base,
+                          int32_t* split_count, int32_t* total_splits, void* stream);
+
 /* Ragged multi-sequence decode over one shared cache: sequence b occupies
  * slots [seq_offset[b], seq_offset[b] + seq_len[b]).  `work`, split_base and
- * split_count are the device copies of bt_ragged_plan's output.  No reference
+ * split_count are the device copies of bt_ragged_plan's output, or
+ * bt_ragged_plan_device's tables (then num_work = total_splits = its
+ * work_capacity).  No reference
  * counterpart (the reference decodes one sequence); it generalises
  * gqa_decode's split/combine (attention.py:54-205) to a per-sequence table. */
 int bt_gqa_decode_ragged(const void* q, int32_t q_dtype, int64_t q_stride_seq, const void* k,

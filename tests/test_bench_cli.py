@@ -26,3 +26,13 @@ def test_modes_are_listed():
     assert r.returncode == 0
     for mode in ("bench", "pmc", "prefill", "ragged", "chunked"):
         assert mode in r.stdout
+
+
+def test_cpu_baseline_helpers():
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    assert bench.cpu_model()
+    calls = []
+    med, n = bench.time_cpu(lambda: calls.append(1), seconds=0.0, min_calls=5)
+    assert n == 5 and len(calls) == 8 and med >= 0.0  # 3 warm-ups + 5 timed

@@ -117,7 +117,8 @@ def test_deterministic(hip_backend):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("seq,ns", [(1000, 1), (1000, 3), (1000, 16), (1000, 40), (100, 16), (4096, 128)])
+@pytest.mark.parametrize("seq,ns", [(1000, 1), (1000, 3), (1000, 16), (1000, 40), (100, 16), (4096, 128),
+                                    (8192, 200), (16384, 256)])
 def test_split_partials_match_oracle(hip_backend, seq, ns):
     """Per-split LSE (log2 domain) and normalised partials against the restated split
     kernel (attention.py:114-166) with the kernel's round-robin dealing of tiles;
@@ -169,13 +170,27 @@ def test_position_past_capacity_is_clamped(hip_backend):
     assert_close(out, orc.torch_attention(case.q.float(), case.k.float(), case.v.float(), case.scale))
 
 
-def test_combine_of_oracle_partials(hip_backend):
-    case = wl.decode_inputs(24, 8, 2, 256, 2000, 2000)
+@pytest.mark.parametrize("seq,ns", [(2000, 37), (9000, 200), (20000, 300)])
+def test_combine_of_oracle_partials(hip_backend, seq, ns):
+    """The combine alone, including its second pass over splits beyond the
+    first 128."""
+    case = wl.decode_inputs(24, 8, 2, 256, seq, seq)
     lse, part = orc.split_decode(case.q.float().numpy(), case.k.float().numpy(),
-                                 case.v.float().numpy(), case.scale, 37)
+                                 case.v.float().numpy(), case.scale, ns)
     out = hip_backend.combine(torch.from_numpy(lse.astype(np.float32)).cuda(),
                               torch.from_numpy(part.astype(np.float32)).cuda())
     assert_close(out, orc.combine_lse(lse, part), atol=1e-5)
+
+
+def test_one_kv_head_at_16k_uses_256_splits(hip_backend):
+    """(8, 1, 256): the split count for one kv head is 256 at 16k context, so the
+    whole call goes through the combine's second pass."""
+    assert hip_backend.pick_splits(1, 16384) == 256
+    case = wl.decode_inputs(29, 8, 1, 256, 16384, 16384)
+    q, k, v = _dev(case.q.float(), case.k, case.v)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device="cuda")
+    ref = orc.torch_attention(case.q.float(), case.k.float(), case.v.float(), case.scale)
+    assert_close(hip_backend.attention_fixed(q, k, v, pos, case.scale), ref)
 
 
 @pytest.mark.parametrize("heads,kv,dim", [(8, 2, 128), (8, 2, 64), (4, 4, 256), (8, 1, 256),

@@ -2,20 +2,28 @@
 the torch f32 reference attention.
 
 A small seeded decoder with the Qwen3.5 attention layer's shape (8 query heads
-with a sigmoid output gate, 2 kv heads, head_dim 256, q/k RMSNorm, RoPE, bf16
-fixed-capacity KV cache written before it is read; breezetoken/model/layers.py:
-55-82, graph.py:35-63, prefill.py:36-80) runs twice on the GPU with every
-operation identical except attention:
+with a sigmoid output gate, 2 kv heads, head_dim 256, q/k RMSNorm, partial
+rotate-half RoPE over the first 64 dims from cos/sin tables, bf16
+fixed-capacity KV cache written before it is read; breezetoken/model/
+layers.py:26-82, graph.py:35-91, prefill.py:36-80) runs on the GPU with every
+operation identical except attention (and, in two variants, the q/k
+preparation):
 
-* HIP path: ``HipBackend.attention_prefill`` for the prompt and
-  ``attention_fixed`` (device position tensor, the graph-decode operator) for
-  every generated token;
 * reference path: the restated ``_torch_attention`` / causal SDPA of the oracle
-  in f32 on the CPU, fed the same bf16 cache contents (backends.py:196-215,
-  prefill.py:56-68).
+  in f32 on the CPU (backends.py:196-215, prefill.py:56-68), fed q in f32 as
+  the reference computes it and the same bf16 cache contents;
+* HIP paths: ``HipBackend.attention_prefill`` on the same f32 q for the prompt,
+  then ``attention_fixed`` (device position, the graph-decode operator) per
+  token -- eagerly; eagerly with the fused ``attn_prep`` launch for q/k
+  norm + RoPE + cache writes (layers.py:58-73); and as the reference's graph
+  step (graph.py:65-141): the whole decode step -- embedding lookup from a
+  device token buffer, every layer with ``attn_prep`` and ``attention_fixed``,
+  the logits, the argmax written back into the token buffer and the device
+  position increment -- captured once in one hipGraph and replayed per token.
 
-Both paths must produce the same 64 token ids.  The smallest top-1/top-2 logit
-margin of the reference run is printed so a near-tie would be visible.
+The logits head is unscaled (random weights of the same fan-in scaling as the
+other projections), so top-1 margins are those of an untrained model; the
+smallest margin of the reference run is printed beside the result.
 """
 
 from __future__ import annotations
@@ -26,11 +34,13 @@ import pytest
 import torch
 
 from oracle import attention as orc
+from oracle import prep as orp
 
 pytestmark = pytest.mark.gpu
 
 VOCAB, HIDDEN, LAYERS, FFN = 4096, 1024, 4, 2048
 H, HKV, D = 8, 2, 256
+ROPE_DIM, THETA, EPS = 64, 1.0e7, 1e-6
 PROMPT, NEW = 16, 64
 CAP = 256  # KV cache slots
 
@@ -55,61 +65,54 @@ def _params(device):
             "w_down": w(HIDDEN, FFN, fan_in=FFN),
         })
     emb = w(VOCAB, HIDDEN, fan_in=1) * 0.5
-    head = w(VOCAB, HIDDEN, fan_in=HIDDEN) * 4.0  # sharper logits: clear top-1 margins
+    head = w(VOCAB, HIDDEN, fan_in=HIDDEN)
     prompt = torch.randint(0, VOCAB, (PROMPT,), generator=g)
     return layers, emb, head, prompt
 
 
-def _rms(x, w, eps=1e-6):
+def _rms(x, w, eps=EPS):
     return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
 
 
-def _rope(x, pos):
-    """x (T, heads, D), pos (T,) int -> rotary embedding over the full head dim."""
-    half = D // 2
-    inv = 1.0 / (10000.0 ** (torch.arange(half, device=x.device, dtype=torch.float32) / half))
-    ang = pos.to(torch.float32)[:, None] * inv[None, :]
-    cos, sin = ang.cos()[:, None, :], ang.sin()[:, None, :]
-    x1, x2 = x[..., :half], x[..., half:]
-    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)
-
-
-def _rope_tab(x, positions, cos, sin):
-    """The same rotation from (CAP, D) tables (layers.py:26-32, backends.py:218-226)."""
-    half = D // 2
+def _rope(x, positions, cos, sin):
+    """Partial rotate-half RoPE on the first ROPE_DIM dims (backends.py:218-226)."""
+    half = ROPE_DIM // 2
+    rot, tail = x[..., :ROPE_DIM], x[..., ROPE_DIM:]
     c, s_ = cos[positions][:, None, :], sin[positions][:, None, :]
-    return x * c + torch.cat((-x[..., half:], x[..., :half]), dim=-1) * s_
+    turned = rot * c + torch.cat((-rot[..., half:], rot[..., :half]), dim=-1) * s_
+    return torch.cat((turned, tail), dim=-1)
 
 
 class _Decoder:
-    def __init__(self, params, attn_prefill, attn_decode, device, tables=None, prep_decode=None):
+    """attn_prefill(q (T, H, D) f32, k, v, scale); attn_decode(q (H, D), kc, vc,
+    pos, scale); prep(qkv, layer params, k cache, v cache, pos) -> (q, gate) or
+    None for the torch q/k preparation."""
+
+    def __init__(self, params, tables, attn_prefill, attn_decode, device, prep=None):
         self.layers, self.emb, self.head, _ = params
-        self.attn_prefill, self.attn_decode = attn_prefill, attn_decode
-        self.tables, self.prep_decode = tables, prep_decode
+        self.cos, self.sin = tables
+        self.attn_prefill, self.attn_decode, self.prep = attn_prefill, attn_decode, prep
         self.device = device
         self.k = [torch.zeros(CAP, HKV * D, dtype=torch.bfloat16, device=device) for _ in range(LAYERS)]
         self.v = [torch.zeros(CAP, HKV * D, dtype=torch.bfloat16, device=device) for _ in range(LAYERS)]
         self.pos = torch.zeros(1, dtype=torch.int32, device=device)
+        self.token = torch.zeros(1, dtype=torch.int64, device=device)
 
     def _block(self, i, x, positions, decode: bool):
         p = self.layers[i]
         t = x.shape[0]
         qkv = _rms(x, p["norm"]) @ p["w_qkv"].T
-        if decode and self.prep_decode is not None:
+        if decode and self.prep is not None:
             # q/k norm + RoPE + cache writes at the device position in one call
-            q, gate = self.prep_decode(qkv.reshape(-1), p, self.k[i], self.v[i], self.pos)
+            q, gate = self.prep(qkv.reshape(-1), p, self.k[i], self.v[i], self.pos)
             q, gate = q.reshape(1, H, D), gate.reshape(1, H, D)
         else:
             qg = qkv[:, : H * 2 * D].reshape(t, H, 2 * D)
             q, gate = qg[..., :D], qg[..., D:]
             k = qkv[:, H * 2 * D : H * 2 * D + HKV * D].reshape(t, HKV, D)
             v = qkv[:, H * 2 * D + HKV * D :].reshape(t, HKV, D)
-            if self.tables is not None:
-                q = _rope_tab(_rms(q, p["q_norm"]), positions, *self.tables)
-                k = _rope_tab(_rms(k, p["k_norm"]), positions, *self.tables)
-            else:
-                q = _rope(_rms(q, p["q_norm"]), positions)
-                k = _rope(_rms(k, p["k_norm"]), positions)
+            q = _rope(_rms(q, p["q_norm"]), positions, self.cos, self.sin)
+            k = _rope(_rms(k, p["k_norm"]), positions, self.cos, self.sin)
             self.k[i][positions] = k.reshape(t, -1).to(torch.bfloat16)  # write before read
             self.v[i][positions] = v.reshape(t, -1).to(torch.bfloat16)
         kc = self.k[i].view(CAP, HKV, D)
@@ -117,7 +120,7 @@ class _Decoder:
         if decode:
             out = self.attn_decode(q.reshape(H, D), kc, vc, self.pos, D**-0.5).reshape(1, H, D)
         else:
-            out = self.attn_prefill(q, kc[:t], vc[:t], D**-0.5)
+            out = self.attn_prefill(q.contiguous(), kc[:t], vc[:t], D**-0.5)
         out = out * torch.sigmoid(gate)
         x = x + out.reshape(t, H * D) @ p["w_o"].T
         h = _rms(x, p["norm2"])
@@ -126,13 +129,28 @@ class _Decoder:
     def _logits(self, x):
         return _rms(x, torch.ones(HIDDEN, device=self.device)) @ self.head.T
 
-    def generate(self, prompt):
-        ids = prompt.to(self.device)
-        x = self.emb[ids]
+    def prefill(self, prompt):
+        x = self.emb[prompt.to(self.device)]
         positions = torch.arange(PROMPT, device=self.device)
         for i in range(LAYERS):
             x = self._block(i, x, positions, decode=False)
-        logits = self._logits(x[-1:])
+        return self._logits(x[-1:])
+
+    def step(self):
+        """One decode step on device state only (graph.py:65-91): the token at
+        self.token, position self.pos; leaves the argmax in self.token and
+        advances self.pos."""
+        x = self.emb.index_select(0, self.token)
+        positions = self.pos.long()
+        for i in range(LAYERS):
+            x = self._block(i, x, positions, decode=True)
+        logits = self._logits(x)
+        self.token.copy_(logits.argmax(dim=-1).reshape(1))
+        self.pos.add_(1)
+        return logits
+
+    def generate_eager(self, prompt):
+        logits = self.prefill(prompt)
         out, margins = [], []
         for step in range(NEW):
             top = torch.topk(logits[0], 2)
@@ -141,19 +159,38 @@ class _Decoder:
             out.append(tok)
             if step == NEW - 1:
                 break
-            pos = PROMPT + step
-            self.pos.fill_(pos)
-            x = self.emb[torch.tensor([tok], device=self.device)]
-            for i in range(LAYERS):
-                x = self._block(i, x, torch.tensor([pos], device=self.device), decode=True)
-            logits = self._logits(x)
+            self.token.fill_(tok)
+            self.pos.fill_(PROMPT + step)
+            logits = self.step()
         return out, margins
+
+    def generate_graph(self, prompt):
+        """Prefill eagerly, then capture step() once and replay it per token."""
+        logits = self.prefill(prompt)
+        first = int(logits[0].argmax())
+        self.token.fill_(first)
+        self.pos.fill_(PROMPT)
+        self.step()  # warm-up (workspaces, library handles); writes the same slot the replay rewrites
+        torch.cuda.synchronize()
+        self.token.fill_(first)
+        self.pos.fill_(PROMPT)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.step()
+        out = [first]
+        for _ in range(NEW - 1):
+            graph.replay()
+            out.append(int(self.token.item()))  # synchronises between replays
+        return out
+
+
+def _tables(dev):
+    return tuple(t.to(dev) for t in orp.rope_tables(CAP, ROPE_DIM, THETA))
 
 
 def _ref_prefill(q, k, v, scale):
-    # the kernel's inputs: bf16 q, the bf16 cache; reference arithmetic in f32 on the CPU
-    qb = q.to(torch.bfloat16).float().cpu()
-    return orc.torch_prefill_attention(qb, k.float().cpu(), v.float().cpu(), scale).to(q.device)
+    # f32 q as the reference computes it, the bf16 cache; f32 arithmetic on the CPU
+    return orc.torch_prefill_attention(q.float().cpu(), k.float().cpu(), v.float().cpu(), scale).to(q.device)
 
 
 def _ref_decode(q, k, v, pos, scale):
@@ -162,51 +199,63 @@ def _ref_decode(q, k, v, pos, scale):
                                scale).to(q.device)
 
 
-def test_greedy_64_tokens_identical(hip_backend):
-    dev = torch.device("cuda")
-    params = _params(dev)
-    prompt = params[3]
+def _reference_ids(params, tables, dev, tag):
+    print(f"[{tag}] reference path", flush=True)
+    ids, margins = _Decoder(params, tables, _ref_prefill, _ref_decode, dev).generate_eager(params[3])
+    print(f"[{tag}] reference: min top-1 margin {min(margins):.4f}, distinct ids {len(set(ids))}", flush=True)
+    return ids
 
-    def hip_prefill(q, k, v, scale):
-        return hip_backend.attention_prefill(q.to(torch.bfloat16), k, v, scale, torch.float32)
 
-    def hip_decode(q, k, v, pos, scale):
+def _first_divergence(a, b):
+    return next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), None)
+
+
+def _hip_fns(hip_backend, tables):
+    cos, sin = tables
+
+    def prefill(q, k, v, scale):
+        assert q.dtype == torch.float32
+        return hip_backend.attention_prefill(q, k, v, scale, torch.float32)
+
+    def decode(q, k, v, pos, scale):
         return hip_backend.attention_fixed(q.float().contiguous(), k, v, pos, scale)
 
-    print("[greedy] reference path", flush=True)
-    ref_ids, margins = _Decoder(params, _ref_prefill, _ref_decode, dev).generate(prompt)
-    print("[greedy] HIP path", flush=True)
-    hip_ids, _ = _Decoder(params, hip_prefill, hip_decode, dev).generate(prompt)
-    print(f"[greedy] min top-1 margin {min(margins):.4f}, distinct ids {len(set(ref_ids))}", flush=True)
+    def prep(qkv, p, kc, vc, pos):
+        return hip_backend.attn_prep(qkv.contiguous(), p["q_norm"], p["k_norm"], EPS, cos, sin, pos, ROPE_DIM,
+                                     kc, vc, H, HKV, D)
+
+    return prefill, decode, prep
+
+
+def test_greedy_64_tokens_identical(hip_backend):
+    dev = torch.device("cuda")
+    params, tables = _params(dev), _tables(dev)
+    ref_ids = _reference_ids(params, tables, dev, "greedy")
+    prefill, decode, _ = _hip_fns(hip_backend, tables)
+    hip_ids, _ = _Decoder(params, tables, prefill, decode, dev).generate_eager(params[3])
     assert len(hip_ids) == NEW
-    assert hip_ids == ref_ids, f"first divergence at step {next(i for i, (a, b) in enumerate(zip(hip_ids, ref_ids)) if a != b)}"
+    assert hip_ids == ref_ids, f"first divergence at step {_first_divergence(hip_ids, ref_ids)}"
 
 
 def test_greedy_64_tokens_identical_with_fused_decode_prep(hip_backend):
-    """As above, and the HIP path also runs each decode step's q/k RMSNorm,
-    RoPE and bf16 cache writes as one ``attn_prep`` launch (layers.py:58-73)
-    instead of the torch operators; both paths rotate with the same tables."""
-    from oracle import prep as orp
-
+    """As above, and the HIP path runs each decode step's q/k RMSNorm, partial
+    RoPE and bf16 cache writes as one ``attn_prep`` launch."""
     dev = torch.device("cuda")
-    params = _params(dev)
-    prompt = params[3]
-    cos, sin = (t.to(dev) for t in orp.rope_tables(CAP, D, 10000.0))
+    params, tables = _params(dev), _tables(dev)
+    ref_ids = _reference_ids(params, tables, dev, "greedy+prep")
+    prefill, decode, prep = _hip_fns(hip_backend, tables)
+    hip_ids, _ = _Decoder(params, tables, prefill, decode, dev, prep=prep).generate_eager(params[3])
+    assert hip_ids == ref_ids, f"first divergence at step {_first_divergence(hip_ids, ref_ids)}"
 
-    def hip_prefill(q, k, v, scale):
-        return hip_backend.attention_prefill(q.to(torch.bfloat16), k, v, scale, torch.float32)
 
-    def hip_decode(q, k, v, pos, scale):
-        return hip_backend.attention_fixed(q.float().contiguous(), k, v, pos, scale)
-
-    def hip_prep(qkv, p, kc, vc, pos):
-        return hip_backend.attn_prep(qkv.contiguous(), p["q_norm"], p["k_norm"], 1e-6, cos, sin, pos, D,
-                                     kc, vc, H, HKV, D)
-
-    print("[greedy+prep] reference path", flush=True)
-    ref_ids, margins = _Decoder(params, _ref_prefill, _ref_decode, dev, tables=(cos, sin)).generate(prompt)
-    print("[greedy+prep] HIP path", flush=True)
-    hip_ids, _ = _Decoder(params, hip_prefill, hip_decode, dev, tables=(cos, sin),
-                          prep_decode=hip_prep).generate(prompt)
-    print(f"[greedy+prep] min top-1 margin {min(margins):.4f}, distinct ids {len(set(ref_ids))}", flush=True)
-    assert hip_ids == ref_ids, f"first divergence at step {next(i for i, (a, b) in enumerate(zip(hip_ids, ref_ids)) if a != b)}"
+def test_greedy_64_tokens_identical_graph_step(hip_backend):
+    """The reference's graph decode (graph.py:65-141): one capture of the whole
+    step, 63 replays, the next token fed back through a device buffer."""
+    dev = torch.device("cuda")
+    params, tables = _params(dev), _tables(dev)
+    ref_ids = _reference_ids(params, tables, dev, "greedy-graph")
+    prefill, decode, prep = _hip_fns(hip_backend, tables)
+    print("[greedy-graph] HIP path: capture once, replay 63x", flush=True)
+    hip_ids = _Decoder(params, tables, prefill, decode, dev, prep=prep).generate_graph(params[3])
+    assert len(hip_ids) == NEW
+    assert hip_ids == ref_ids, f"first divergence at step {_first_divergence(hip_ids, ref_ids)}"
