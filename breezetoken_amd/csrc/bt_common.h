@@ -73,6 +73,10 @@ __device__ __forceinline__ bf16x8 lds_read_tr_pair(const BT_LDS uint16_t* p0, co
   return as_bf16x8(r);
 }
 
+// max(a, b) that propagates NaN: one v_maximum_f32 on gfx950, with none of the
+// operand canonicalisation fmaxf needs in IEEE mode (-inf stays the identity).
+__device__ __forceinline__ float fmax_nc(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 __device__ __forceinline__ float wave_max_xor(float x, int mask) {
   return fmaxf(x, __shfl_xor(x, mask, 64));
 }
@@ -82,13 +86,13 @@ __device__ __forceinline__ float wave_max_xor(float x, int mask) {
 // {x[0..31], x[0..31]} and {x[32..63], x[32..63]}.
 __device__ __forceinline__ float halves_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return fmax_nc(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 // Max of x over lanes l and l ^ 16 with one v_permlane16_swap (gfx950): it
 // swaps the odd 16-lane rows of one copy with the even rows of another.
 __device__ __forceinline__ float rows16_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return fmax_nc(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float halves_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -260,7 +260,16 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
 
   // S^T = K.Q^T on the K tile kb, mask, online softmax: P^T of the step in pk.
   u32x4 pk[NQT];
-  auto qk_sm = [&](const unsigned char* kb, int u) {
+  // Block scales (V^T and K exponents) of a step's unit, read one step ahead
+  // into scalar registers so the softmax never waits for them.  Steps past this
+  // group's range read the last block's (their values are unused).
+  auto unit_scales = [&](int u, int& eb, int& ek) {
+    int b64 = unit_key(u) * kUnit / kPrefillKeyBlock;
+    b64 = b64 < 0 ? 0 : (b64 < nblk64 ? b64 : nblk64 - 1);
+    eb = sload(vexp, b64);
+    ek = sload(kexp, b64);
+  };
+  auto qk_sm = [&](const unsigned char* kb, int u, int eb, int ek) {
     const int blk = unit_blk(u);
     const int key0 = unit_key(u) * kUnit;
     floatx4 sacc[2][NQT];
@@ -311,8 +320,6 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     // The V^T tile's scale: e of its 64-key block (wave-uniform).  P enters
     // P.V as P' = P * 2^shift (the shift rides in the exp2 bias); the row sum
     // takes P, i.e. the sum of P' times 2^-shift.
-    const int eb = sload(vexp, key0 / kPrefillKeyBlock);
-    const int ek = sload(kexp, key0 / kPrefillKeyBlock);  // the K block's scale
     const int e_new = vexp_next(e_run, eb);
     const int shift = vexp_shift(e_new, eb);
     const float dshift = (float)shift;
@@ -321,7 +328,8 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       const floatx4& s0 = sacc[0][t];
       const floatx4& s1 = sacc[1][t];
       const float c_log2 = __builtin_ldexpf(c_col[t], ek);  // log2-domain factor of the scaled scores
-      float tmax = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+      float tmax = fmax_nc(fmax_nc(fmax_nc(s0[0], s0[1]), fmax_nc(s0[2], s0[3])),
+                           fmax_nc(fmax_nc(s1[0], s1[1]), fmax_nc(s1[2], s1[3])));
       tmax = rows16_max(tmax);
       tmax = halves_max(tmax) * c_log2;
       const bool move = tmax > m_ref[t] + kLazyP;
@@ -396,7 +404,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // Copies go out as soon as their buffer is free: A requests K and V^T of
   // step st + 1 at the first barrier of st; B requests K of st + 1 at the first
   // barrier and V^T of st + 1 at the second (after its P.V of st - 1).
-  auto step = [&](auto bufsel, int st) {
+  auto step = [&](auto bufsel, int st, int& eb, int& ek) {
     constexpr bool kOdd = decltype(bufsel)::value;
     unsigned char* Kc = kOdd ? K1 : K0;   // this step's buffers
     unsigned char* Vc = kOdd ? V1 : V0;
@@ -408,30 +416,40 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     if constexpr (GRP == 0) {
       wait_tiles(1);  // K of st (its V^T was issued after it)
       barrier();
+      int eb_n, ek_n;
+      unit_scales(st + 1, eb_n, ek_n);
       if (w1) { copy_k(Kn, st + 1); copy_v(Vn, st + 1); }
       __builtin_amdgcn_s_setprio(1);
-      if (w0) qk_sm(Kc, st);
+      if (w0) qk_sm(Kc, st, eb, ek);
       __builtin_amdgcn_s_setprio(0);
+      eb = eb_n;
+      ek = ek_n;
       wait_tiles(w1 ? 2 : 0);  // V^T of st (behind it: K and V^T of st + 1)
       barrier();
       if (w0) pv(Vc);
     } else {
       wait_tiles(w0 ? 2 : 0);  // V^T of st - 1 (behind it: K and V^T of st)
       barrier();
+      int eb_n, ek_n;
+      unit_scales(st + 1, eb_n, ek_n);
       if (w1) copy_k(Kn, st + 1);
       if (working(st - 1)) pv(Vn);
       wait_tiles((w0 ? 1 : 0) + (w1 ? 1 : 0));  // K of st (behind it: V^T of st, K of st + 1)
       barrier();
       if (w1) copy_v(Vn, st + 1);
       __builtin_amdgcn_s_setprio(1);
-      if (w0) qk_sm(Kc, st);
+      if (w0) qk_sm(Kc, st, eb, ek);
       __builtin_amdgcn_s_setprio(0);
+      eb = eb_n;
+      ek = ek_n;
     }
   };
   auto run = [&](int s0, int s1) {  // s0 and s1 even
+    int eb, ek;
+    unit_scales(s0, eb, ek);
     for (int st = s0; st < s1; st += 2) {
-      step(Sel<false>{}, st);
-      step(Sel<true>{}, st + 1);
+      step(Sel<false>{}, st, eb, ek);
+      step(Sel<true>{}, st + 1, eb, ek);
     }
   };
   if constexpr (GRP == 0) {
