@@ -247,6 +247,41 @@ def chunked_mode(torch, backend, dev, calls: int) -> int:
     return 0
 
 
+def decode_mode(torch, backend, dev, calls: int, valid: int) -> int:
+    """Config-2 fixed-capacity decode at one valid length only (for rocprofv3
+    kernel traces of split vs combine): ``calls`` calls rotating over six layer
+    caches (384 MiB, past the MALL) after two warm-up rounds, timed with HIP
+    events on the current stream."""
+    from breezetoken_amd import workloads as wl
+    from breezetoken_amd.kvcache import KVCache
+
+    cap = 65536
+    case = wl.c2_inputs(valid, cap=cap)
+    layers = []
+    for _ in range(6):
+        cache = KVCache(cap, case.k.shape[1], case.k.shape[2], dev)
+        cache.k.copy_(case.k.reshape(cap, -1))
+        cache.v.copy_(case.v.reshape(cap, -1))
+        layers.append((cache,) + cache.views())
+    q = case.q.float().to(dev)
+    pos = torch.tensor([case.pos], dtype=torch.int32, device=dev)
+    for i in range(12):
+        _, k, v = layers[i % 6]
+        backend.attention_fixed(q, k, v, pos, case.scale)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(torch.cuda.current_stream())
+    for i in range(calls):
+        _, k, v = layers[i % 6]
+        backend.attention_fixed(q, k, v, pos, case.scale)
+    end.record(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / calls
+    print(json.dumps({"mode": "decode", "valid": valid, "calls": calls, "us_per_call_eager": round(us, 2),
+                      "num_split": backend.pick_splits(case.k.shape[1], cap)}), flush=True)
+    return 0
+
+
 def ragged_mode(torch, backend, dev, calls: int) -> int:
     """Config-5 ragged decode only (for rocprofv3 kernel traces): ``calls`` calls
     over three copies of the cache after two warm-up calls, timed with HIP events
@@ -288,10 +323,12 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--q-f32", action="store_true", help="prefill mode: f32 q (the reference's prefill arithmetic)")
-    ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "ragged", "chunked"], default="bench",
+    ap.add_argument("--valid", type=int, default=32768, help="decode mode: valid length (config 2)")
+    ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "decode", "ragged", "chunked"], default="bench",
                     help="pmc: only a 256 MiB device copy and the config-2 split kernel, "
                          "5 launches each, for rocprofv3 --pmc runs; prefill: only config-4 "
-                         "prefill at S=8192 (--steps calls), for kernel traces; ragged: only "
+                         "prefill at S=8192 (--steps calls), for kernel traces; decode: only "
+                         "config-2 decode at --valid (--steps calls), for kernel traces; ragged: only "
                          "config-5 ragged decode (--steps calls), for kernel traces; chunked: "
                          "only the split-key prefill shapes (--steps calls each), for kernel traces")
     args = ap.parse_args()
@@ -319,6 +356,8 @@ def main() -> int:
         return pmc_mode(torch, backend, dev)
     if args.mode == "prefill":
         return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)), args.q_f32)
+    if args.mode == "decode":
+        return decode_mode(torch, backend, dev, max(1, min(args.steps, 2000)), args.valid)
     if args.mode == "ragged":
         return ragged_mode(torch, backend, dev, max(1, min(args.steps, 500)))
     if args.mode == "chunked":

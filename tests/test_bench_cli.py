@@ -24,7 +24,7 @@ def test_more_than_one_gpu_exits_with_a_message():
 def test_modes_are_listed():
     r = _run("--help")
     assert r.returncode == 0
-    for mode in ("bench", "pmc", "prefill", "ragged", "chunked"):
+    for mode in ("bench", "pmc", "prefill", "decode", "ragged", "chunked"):
         assert mode in r.stdout
 
 
