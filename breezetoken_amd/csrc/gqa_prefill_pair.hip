@@ -186,24 +186,76 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // past the prompt read the last row (their output is not stored).
   u32x4 qop[NQT][kDSteps];
   float c_col[NQT];
+  // One pass over q: every load of the block is issued before any is used (the
+  // raw values take the registers O frees between blocks), then each row's
+  // largest |q| is reduced over its four lane groups and the values converted.
+  auto row_scale = [&](int t, uint32_t mx) {
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+    const int eq = absmax_exp(mx);
+    c_col[t] = __builtin_ldexpf(p.scale_log2, eq);
+    return eq;
+  };
   auto load_q = [&](int blk) {
+    int64_t off[NQT];
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
       const int row = min(blk * sh.pos + poff[t] + i16, S - 1);
-      const int64_t off = (int64_t)row * p.q_stride_tok + (int64_t)head[t] * p.q_stride_head + g4 * 8;
-      const bool f32 = p.q_f32 != 0;
-      uint32_t mx = 0;
+      off[t] = (int64_t)row * p.q_stride_tok + (int64_t)head[t] * p.q_stride_head + g4 * 8;
+    }
+    if (p.q_f32) {
+      const float* qf = reinterpret_cast<const float*>(p.q);
+      float4 raw[NQT][kDSteps][2];
 #pragma unroll
-      for (int st = 0; st < kDSteps; ++st) mx = max(mx, q_chunk_absmax(p.q, f32, off + st * 32));
-      mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
-      mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
-      const int eq = absmax_exp(mx);
-      c_col[t] = __builtin_ldexpf(p.scale_log2, eq);
+      for (int t = 0; t < NQT; ++t)
 #pragma unroll
-      for (int st = 0; st < kDSteps; ++st) qop[t][st] = q_chunk_f16(p.q, f32, off + st * 32, eq);
+        for (int st = 0; st < kDSteps; ++st) {
+          raw[t][st][0] = *reinterpret_cast<const float4*>(qf + off[t] + st * 32);
+          raw[t][st][1] = *reinterpret_cast<const float4*>(qf + off[t] + st * 32 + 4);
+        }
+#pragma unroll
+      for (int t = 0; t < NQT; ++t) {
+        uint32_t mx = 0;
+#pragma unroll
+        for (int st = 0; st < kDSteps; ++st)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float4 v = raw[t][st][h];
+            mx = max(mx, max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
+                             max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu)));
+          }
+        const int eq = row_scale(t, mx);
+#pragma unroll
+        for (int st = 0; st < kDSteps; ++st) {
+          const float4 a = raw[t][st][0], b = raw[t][st][1];
+          qop[t][st] = u32x4{pack_f16x2_scaled(a.x, a.y, eq), pack_f16x2_scaled(a.z, a.w, eq),
+                             pack_f16x2_scaled(b.x, b.y, eq), pack_f16x2_scaled(b.z, b.w, eq)};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NQT; ++t)
+#pragma unroll
+        for (int st = 0; st < kDSteps; ++st) qop[t][st] = *reinterpret_cast<const u32x4*>(p.q + off[t] + st * 32);
+#pragma unroll
+      for (int t = 0; t < NQT; ++t) {
+        uint32_t mx = 0;
+#pragma unroll
+        for (int st = 0; st < kDSteps; ++st)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = max(mx, max((qop[t][st][i] << 16) & 0x7fffffffu, qop[t][st][i] & 0x7fff0000u));
+        const int eq = row_scale(t, mx);
+#pragma unroll
+        for (int st = 0; st < kDSteps; ++st) {
+          const u32x4 w = qop[t][st];
+          qop[t][st] = u32x4{pack_f16x2_scaled(__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u), eq),
+                             pack_f16x2_scaled(__uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u), eq),
+                             pack_f16x2_scaled(__uint_as_float(w[2] << 16), __uint_as_float(w[2] & 0xffff0000u), eq),
+                             pack_f16x2_scaled(__uint_as_float(w[3] << 16), __uint_as_float(w[3] & 0xffff0000u), eq)};
+        }
+      }
     }
   };
-
   // ---- running state: per q-tile column (this lane's i16) -------------------
   floatx4 oacc[NQT][kDTiles];
   float m_ref[NQT], l_run[NQT];
