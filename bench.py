@@ -512,6 +512,14 @@ def main() -> int:
                     torch, lambda: backend.attention_prefill(qc, kc, vc, 256**-0.5, torch.bfloat16,
                                                              q_offset=pos0, split_keys=split),
                     max(20, esteps // 10), 5)
+            if pos0 > 0:
+                # steady state of a chunk loop with the images kept (only this chunk's blocks converted)
+                imgs = backend.prefill_images(pos0 + steps, 2, 256)
+                row["us_split_kept_images"] = 1e3 * time_graph(
+                    torch, lambda: backend.attention_prefill(qc, kc, vc, 256**-0.5, torch.bfloat16,
+                                                             q_offset=pos0, images=imgs),
+                    max(20, esteps // 10), 5)
+                del imgs
             fl = 2 * heads * 256 * steps * (steps + 2 * pos0 + 1)
             row["TFLOPs_split"] = fl / (row["us_split"] * 1e-6) / 1e12
             chunked.append(row)

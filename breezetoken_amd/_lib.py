@@ -71,6 +71,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _c_i32, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
          _c_f32, _vp, _c_i64, _vp, _c_i32, _c_i64, _c_i64, _vp],
     ),
+    "bt_prefill_partials_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "bt_gqa_prefill_cached": (
+        ctypes.c_int,
+        [_vp, _c_i32, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+         _c_f32, _vp, _c_i64, _c_i32, _c_i32, _vp, _c_i64, _vp, _c_i32, _c_i64, _c_i64, _vp],
+    ),
     "bt_rms_norm_rope": (
         ctypes.c_int,
         [_vp, _c_i64, _c_i32, _c_i32, _vp, _c_f32, _vp, _vp, _vp, _c_i32, _c_i32, _vp, _c_i64, _vp],

@@ -460,9 +460,15 @@ class HipBackend:
         return out
 
     # ------------------------------------------------------------------ prefill
+    def prefill_images(self, capacity: int, kv_heads: int, head_dim: int) -> "PrefillImages":
+        """Persistent K / V^T images for chunked prefill over one cache of
+        ``capacity`` slots (see ``PrefillImages``)."""
+        return PrefillImages(self, capacity, kv_heads, head_dim)
+
     def attention_prefill(
         self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
         out_dtype: torch.dtype = torch.float32, q_offset: int = 0, split_keys: bool = True,
+        images: "PrefillImages | None" = None,
     ) -> torch.Tensor:
         """Causal GQA prefill: q (S, H, D) are the new tokens at positions
         q_offset .. q_offset + S - 1 (f32, as the reference computes it, or bf16),
@@ -470,8 +476,11 @@ class HipBackend:
         strides) -> (S, H, D); row i attends keys
         0 .. q_offset + i.  q_offset = 0 is the SDPA call of prefill.py:56-68, a
         positive one the banded-mask chunked prefill of qwen36_moe.py:394-428.
-        ``split_keys=False`` hands the library only the V^T workspace, which keeps
-        one work-group per query block (for comparisons; results agree to ~1e-6)."""
+        ``split_keys=False`` hands the library only the image workspace, which keeps
+        one work-group per query block (for comparisons; results agree to ~1e-6).
+        ``images`` (a ``PrefillImages`` of this cache) keeps the K / V^T images
+        across the chunks of one sequence, so each call converts only the
+        blocks from its own first key on; results equal the call without it."""
         if q.ndim != 3 or k.ndim != 3 or v.shape != k.shape:
             raise ValueError("prefill expects q (S, H, D), k/v (q_offset + S, Hkv, D)")
         steps, heads, dim = q.shape
@@ -489,6 +498,8 @@ class HipBackend:
         if k.stride() != v.stride():
             raise RuntimeError("k and v need identical strides")
         out = torch.empty((steps, heads, dim), dtype=out_dtype, device=self._dev)
+        if images is not None:
+            return images._run(q, k, v, scale, out, q_offset, split_keys)
         ws = self._prefill_workspace(steps, q_offset, heads, groups, dim)
         ws_len = ws.numel()
         if not split_keys:
@@ -505,14 +516,14 @@ class HipBackend:
 
     def sdpa_prefill(
         self, qq: torch.Tensor, kk: torch.Tensor, vv: torch.Tensor, scale: float,
-        out_dtype: torch.dtype = torch.float32, q_offset: int = 0,
+        out_dtype: torch.dtype = torch.float32, q_offset: int = 0, images: "PrefillImages | None" = None,
     ) -> torch.Tensor:
         """Drop-in for the SDPA calls of prefill.py:60-68 (q_offset = 0) and
         qwen36_moe.py:415-423 (q_offset = pos0, head-major cache views):
         qq (1, H, S, D), kk/vv (1, Hkv, q_offset + S, D) -> (1, H, S, D)."""
         out = self.attention_prefill(
             qq[0].transpose(0, 1), kk[0].transpose(0, 1), vv[0].transpose(0, 1), scale, out_dtype,
-            q_offset=q_offset,
+            q_offset=q_offset, images=images,
         )
         return out.transpose(0, 1).unsqueeze(0)
 
@@ -702,6 +713,55 @@ class HipBackend:
 
     def __repr__(self) -> str:
         return f"HipBackend(device={self.device!r}, arch={self.arch!r}, cus={self.num_cus})"
+
+
+class PrefillImages:
+    """The block-scaled fp16 K and V^T images of one layer's cache, kept across
+    the chunks of a chunked prefill (qwen36_moe.py:394-428 runs one prefill call
+    per chunk at growing ``pos0``): each call converts only the 64-key blocks
+    from its own first key on, instead of the whole cached prefix.
+
+    The images are valid for the cache (data pointer and strides) they were
+    built from and for keys below ``valid_keys``; a call on another cache, or
+    at a ``q_offset`` below ``valid_keys`` (a rewound sequence), rebuilds from
+    ``min(valid_keys, q_offset)`` or from 0.  The caller must not change cached
+    keys below ``valid_keys`` between calls (``reset()`` forgets them)."""
+
+    def __init__(self, backend: HipBackend, capacity: int, kv_heads: int, head_dim: int) -> None:
+        self._be = backend
+        self.capacity, self.kv_heads, self.head_dim = int(capacity), int(kv_heads), int(head_dim)
+        nbytes = int(backend._lib.bt_prefill_workspace_bytes(self.capacity, self.kv_heads, self.head_dim))
+        if nbytes <= 0:
+            raise RuntimeError("invalid image shape")
+        self.buf = torch.empty(nbytes, dtype=torch.uint8, device=backend._dev)
+        self.valid_keys = 0
+        self._source: tuple | None = None
+
+    def reset(self) -> None:
+        self.valid_keys = 0
+        self._source = None
+
+    def _run(self, q, k, v, scale, out, q_offset: int, split_keys: bool) -> torch.Tensor:
+        be = self._be
+        steps, heads, dim = q.shape
+        groups = k.shape[1]
+        if (groups, dim) != (self.kv_heads, self.head_dim) or q_offset + steps > self.capacity:
+            raise RuntimeError("these images were made for another cache shape or capacity")
+        source = (k.data_ptr(), v.data_ptr(), tuple(k.stride()))
+        cached = min(self.valid_keys, q_offset) if source == self._source else 0
+        pbytes = int(be._lib.bt_prefill_partials_bytes(steps, q_offset, heads, groups, dim)) if split_keys else 0
+        part = be._grow("prefill_partials", pbytes) if pbytes else None
+        rc = be._lib.bt_gqa_prefill_cached(
+            q.data_ptr(), _dtype_code(q.dtype), k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1),
+            k.stride(0), k.stride(1), steps, q_offset, heads, groups, dim, float(scale),
+            self.buf.data_ptr(), self.buf.numel(), self.capacity, cached,
+            _ptr(part), pbytes, out.data_ptr(), _dtype_code(out.dtype), out.stride(0), out.stride(1),
+            _stream(be._dev),
+        )
+        check("bt_gqa_prefill_cached", rc)
+        self._source = source
+        self.valid_keys = q_offset + steps
+        return out
 
 
 def make_backend(kind: str = "hip", device: str = "cuda") -> HipBackend:

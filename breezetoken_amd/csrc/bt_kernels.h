@@ -75,6 +75,8 @@ struct PrefillParams {
   int32_t* vexp;       // workspace: per (kv head, 64-key block) power-of-two scale of the image
   uint16_t* kimg;      // workspace: fp16 K image (row-major, XOR-swizzled slots), prefill_vt_bytes() bytes
   int32_t* kexp;       // workspace: per (kv head, 64-key block) power-of-two scale of the K image
+  int32_t img_blocks;  // 64-key blocks per kv head in the image layout (>= those of q_offset + seqlen keys)
+  int32_t img_first;   // first block the pre-pass converts (the images already hold the earlier ones)
   int32_t q_f32;       // 1: q is f32, 0: bf16 (either enters Q.K^T as fp16 scaled per row)
   // Split-key mode of the two-waves-per-SIMD kernel (kb_chunk > 0): work-group
   // (query block, kv head, chunk c) covers key blocks [c*kb_chunk, +kb_chunk);

@@ -450,13 +450,18 @@ int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32
   return plan.kb_chunk > 0 ? part_offset + (int64_t)plan.part_bytes : vt;
 }
 
-int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,
-                   int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
-                   int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
-                   int32_t head_dim, float scale, void* workspace, int64_t workspace_bytes,
-                   void* out, int32_t out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
-                   void* stream) {
-  if (!q || !k || !v || !out || !workspace) return BT_EINVAL;
+// Shared by bt_gqa_prefill and bt_gqa_prefill_cached: validates the call and
+// launches the pre-pass and the attention kernel.  `images` holds the K / V^T
+// images and their exponents laid out for img_keys keys (prefill_layout); the
+// pre-pass converts the blocks from key img_first_key on.  `partials` (may be
+// null) holds the split-key partials when it is large enough.
+static int prefill_run(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,
+                       int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head, int32_t seqlen,
+                       int32_t q_offset, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
+                       void* images, int32_t img_keys, int32_t img_first_key, void* partials,
+                       int64_t partials_bytes, void* out, int32_t out_dtype, int64_t out_stride_tok,
+                       int64_t out_stride_head, void* stream) {
+  if (!q || !k || !v || !out || !images) return BT_EINVAL;
   if (seqlen < 1 || q_offset < 0 || heads < 1 || kv_heads < 1 || heads % kv_heads) return BT_EINVAL;
   if ((int64_t)q_offset + seqlen > INT32_MAX) return BT_EINVAL;
   if (out_dtype != BT_DTYPE_F32 && out_dtype != BT_DTYPE_BF16) return BT_EINVAL;
@@ -468,18 +473,18 @@ int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v,
   if (q_stride_tok % 8 || q_stride_head % 8 || kv_stride_tok % 8 || kv_stride_head % 8 ||
       out_stride_tok % 8 || out_stride_head % 8)
     return BT_EINVAL;
-  if (!aligned16(workspace)) return BT_EINVAL;
+  if (!aligned16(images) || (partials && !aligned16(partials))) return BT_EINVAL;
   if (head_dim != 256 && head_dim != 128) return BT_ENOTSUP;
   if (heads / kv_heads > 8) return BT_ENOTSUP;
   // 32-bit buffer offsets: the K rows of one kv head (plus the last block's
-  // tail) and its V^T image
+  // tail) and its images
   const int32_t kv_len = q_offset + seqlen;
+  if (img_keys < kv_len || img_first_key < 0 || img_first_key > q_offset) return BT_EINVAL;
   const int64_t nblk = ((int64_t)kv_len + bt::kPrefillKeyBlock - 1) / bt::kPrefillKeyBlock;
+  const int64_t img_blocks = ((int64_t)img_keys + bt::kPrefillKeyBlock - 1) / bt::kPrefillKeyBlock;
   if ((nblk + 1) * bt::kPrefillKeyBlock * kv_stride_tok * 2 > (int64_t)UINT32_MAX ||
-      nblk * bt::kPrefillKeyBlock * head_dim * 2 > (int64_t)UINT32_MAX)
+      img_blocks * bt::kPrefillKeyBlock * head_dim * 2 > (int64_t)UINT32_MAX)
     return BT_ENOTSUP;
-  const bool q_f32 = q_dtype == BT_DTYPE_F32;
-  if (workspace_bytes < bt_prefill_workspace_bytes(kv_len, kv_heads, head_dim)) return BT_ENOSPC;
   bt::PrefillParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k);
@@ -498,31 +503,75 @@ int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v,
   p.out_bf16 = out_dtype == BT_DTYPE_BF16;
   p.out_stride_tok = out_stride_tok;
   p.out_stride_head = out_stride_head;
-  p.vt = static_cast<uint16_t*>(workspace);
-  const PrefillLayout lay = prefill_layout(kv_len, kv_heads, head_dim);
-  p.vexp = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + lay.vexp);
-  p.kimg = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + lay.kimg);
-  p.kexp = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + lay.kexp);
-  p.q_f32 = q_f32 ? 1 : 0;
+  const PrefillLayout lay = prefill_layout(img_keys, kv_heads, head_dim);
+  p.vt = static_cast<uint16_t*>(images);
+  p.vexp = reinterpret_cast<int32_t*>(static_cast<char*>(images) + lay.vexp);
+  p.kimg = reinterpret_cast<uint16_t*>(static_cast<char*>(images) + lay.kimg);
+  p.kexp = reinterpret_cast<int32_t*>(static_cast<char*>(images) + lay.kexp);
+  p.img_blocks = (int32_t)img_blocks;
+  p.img_first = img_first_key / bt::kPrefillKeyBlock;
+  p.q_f32 = q_dtype == BT_DTYPE_F32 ? 1 : 0;
   if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim))
     return hip_rc(bt::launch_prefill_pair(p, head_dim, (hipStream_t)stream));
   // Group sizes 1, 2, 4, 8 at D = 128 / 256 run two waves per SIMD; other
-  // shapes take the one-wave-per-SIMD kernel.  Each writes its own fp16 V^T
-  // image (laid out for its MFMA shape) into the same workspace size.  When
-  // one work-group per query block would leave CUs idle and the workspace
-  // also holds bt_prefill_split_workspace_bytes, the key range is split.
+  // shapes take the one-wave-per-SIMD kernel (each reads the image order its
+  // MFMA shape needs).  When one work-group per query block would leave CUs
+  // idle and `partials` holds the plan's partials, the key range is split.
   if (bt::prefill8_serves(p.group, head_dim)) {
     int64_t part_offset = 0;
     const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
-    if (plan.kb_chunk > 0 && workspace_bytes >= part_offset + (int64_t)plan.part_bytes) {
+    if (plan.kb_chunk > 0 && partials && partials_bytes >= (int64_t)plan.part_bytes) {
       p.kb_chunk = plan.kb_chunk;
       p.max_chunks = plan.max_chunks;
-      p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_offset);
+      p.part = static_cast<float*>(partials);
       p.lse = p.part + plan.part_rows * (size_t)head_dim;
     }
     return hip_rc(bt::launch_prefill8(p, head_dim, (hipStream_t)stream));
   }
   return hip_rc(bt::launch_prefill(p, head_dim, (hipStream_t)stream));
+}
+
+int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,
+                   int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head,
+                   int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
+                   int32_t head_dim, float scale, void* workspace, int64_t workspace_bytes,
+                   void* out, int32_t out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
+                   void* stream) {
+  if (!workspace) return BT_EINVAL;
+  if (seqlen < 1 || q_offset < 0 || heads < 1 || kv_heads < 1 || heads % kv_heads) return BT_EINVAL;
+  if ((int64_t)q_offset + seqlen > INT32_MAX) return BT_EINVAL;
+  const int32_t kv_len = q_offset + seqlen;
+  if (workspace_bytes < bt_prefill_workspace_bytes(kv_len, kv_heads, head_dim)) return BT_ENOSPC;
+  // the split-key partials follow the images (256-byte aligned)
+  const int64_t part_offset = align256(prefill_base_bytes(kv_len, kv_heads, head_dim));
+  void* partials = workspace_bytes > part_offset ? static_cast<char*>(workspace) + part_offset : nullptr;
+  return prefill_run(q, q_dtype, k, v, q_stride_tok, q_stride_head, kv_stride_tok, kv_stride_head, seqlen,
+                     q_offset, heads, kv_heads, head_dim, scale, workspace, kv_len, 0, partials,
+                     partials ? workspace_bytes - part_offset : 0, out, out_dtype, out_stride_tok,
+                     out_stride_head, stream);
+}
+
+int64_t bt_prefill_partials_bytes(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
+                                  int32_t head_dim) {
+  if (seqlen < 1 || q_offset < 0 || heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 1) return 0;
+  if ((int64_t)q_offset + seqlen > INT32_MAX) return 0;
+  int64_t part_offset = 0;
+  const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
+  return plan.kb_chunk > 0 ? (int64_t)plan.part_bytes : 0;
+}
+
+int bt_gqa_prefill_cached(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,
+                          int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head, int32_t seqlen,
+                          int32_t q_offset, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
+                          void* images, int64_t images_bytes, int32_t capacity, int32_t cached_keys,
+                          void* partials, int64_t partials_bytes, void* out, int32_t out_dtype,
+                          int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+  if (capacity < 1 || (int64_t)q_offset + seqlen > capacity) return BT_EINVAL;
+  if (cached_keys < 0 || cached_keys > q_offset) return BT_EINVAL;
+  if (images_bytes < bt_prefill_workspace_bytes(capacity, kv_heads, head_dim)) return BT_ENOSPC;
+  return prefill_run(q, q_dtype, k, v, q_stride_tok, q_stride_head, kv_stride_tok, kv_stride_head, seqlen,
+                     q_offset, heads, kv_heads, head_dim, scale, images, capacity, cached_keys, partials,
+                     partials_bytes, out, out_dtype, out_stride_tok, out_stride_head, stream);
 }
 
 static bool prep_dim_served(int32_t d) { return d == 64 || d == 128 || d == 256 || d == 512; }

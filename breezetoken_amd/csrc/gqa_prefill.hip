@@ -158,10 +158,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
   // l sits in slot i ^ (l & 15)); V^T copy i is bytes [1024 i, +1024) of the
   // block's image.  Wave w issues copies w, w + 4, ...
   constexpr int kRowBytes = D * 2;
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.kimg + (size_t)kvh * nblk * kKB * D, (uint32_t)nblk * kImg);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.vt + (size_t)kvh * nblk * kKB * D, (uint32_t)nblk * kImg);
-  const int* vexp = p.vexp + kvh * nblk;
-  const int* kexp = p.kexp + kvh * nblk;
+  const size_t head_img = (size_t)kvh * p.img_blocks * kKB * D;  // this kv head's images
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.kimg + head_img, (uint32_t)nblk * kImg);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.vt + head_img, (uint32_t)nblk * kImg);
+  const int* vexp = p.vexp + kvh * p.img_blocks;
+  const int* kexp = p.kexp + kvh * p.img_blocks;
   const uint32_t v_voff = (uint32_t)lane * 16;
   auto copy_k = [&](auto b, int kb) {
     const uint32_t so = (uint32_t)kb * kImg;

@@ -125,9 +125,10 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   const int last = kb1 - 1;
   const int head = kvh * G + wave % G;
 
-  const __amdgpu_buffer_rsrc_t krs = rsrc8(p.kimg + (size_t)kvh * nblk * kKB8 * D, (uint32_t)nblk * kImg);
-  const __amdgpu_buffer_rsrc_t vrs = rsrc8(p.vt + (size_t)kvh * nblk * kKB8 * D, (uint32_t)nblk * kImg);
-  const int* kexp = p.kexp + kvh * nblk;
+  const size_t head_img = (size_t)kvh * p.img_blocks * kKB8 * D;  // this kv head's images
+  const __amdgpu_buffer_rsrc_t krs = rsrc8(p.kimg + head_img, (uint32_t)nblk * kImg);
+  const __amdgpu_buffer_rsrc_t vrs = rsrc8(p.vt + head_img, (uint32_t)nblk * kImg);
+  const int* kexp = p.kexp + kvh * p.img_blocks;
   const uint32_t v_voff = (uint32_t)lane * 16;
   // Tile copy i (1 KiB) is bytes [1024 i, +1024) of the block's K or V^T
   // image; the K image is row-major with 16-byte slot s of row r holding chunk
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   float m_ref = -INFINITY;          // reference max (log2 domain) of this lane's query column
   float l_run = 0.f;                // partial row sum over this lane's keys
   int e_run = kVExpZero;            // V scale O is kept in: O_true = O * 2^e_run
-  const int* vexp = p.vexp + kvh * nblk;
+  const int* vexp = p.vexp + kvh * p.img_blocks;
   const int my_q = q0 + i16;
   const int my_pos = P0 + my_q;     // keys 0 .. my_pos
   u32x4 pk[2];                      // P of the pending block: 32-key halves, fp16

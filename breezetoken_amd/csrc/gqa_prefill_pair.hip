@@ -140,10 +140,11 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
 
   const int nblk64 = (nkeys + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
   const uint32_t img_bytes = (uint32_t)nblk64 * kPrefillKeyBlock * kRowBytes;
-  const __amdgpu_buffer_rsrc_t krs = rsrc_p(p.kimg + (size_t)kvh * nblk64 * kPrefillKeyBlock * D, img_bytes);
-  const __amdgpu_buffer_rsrc_t vrs = rsrc_p(p.vt + (size_t)kvh * nblk64 * kPrefillKeyBlock * D, img_bytes);
-  const int* vexp = p.vexp + kvh * nblk64;
-  const int* kexp = p.kexp + kvh * nblk64;
+  const size_t head_img = (size_t)kvh * p.img_blocks * kPrefillKeyBlock * D;  // this kv head's images
+  const __amdgpu_buffer_rsrc_t krs = rsrc_p(p.kimg + head_img, img_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = rsrc_p(p.vt + head_img, img_bytes);
+  const int* vexp = p.vexp + kvh * p.img_blocks;
+  const int* kexp = p.kexp + kvh * p.img_blocks;
 
   // Tile copies: the unit's 32 rows of K (row-major, slots XOR-swizzled by
   // the pre-pass, so the operand reads of 16 consecutive rows hit 16 bank

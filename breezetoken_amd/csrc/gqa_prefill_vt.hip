@@ -30,7 +30,11 @@
 // (columns 8 * (s ^ (r & 15)) ..), the XOR swizzle the kernels' K tiles use in
 // LDS, so a tile copy is a plain contiguous copy.
 //
-// Keys past kv_len are zero in both images.
+// Keys past kv_len are zero in both images.  nblk is the layout's blocks per kv
+// head (p.img_blocks: the blocks of kv_len keys for a per-call workspace, of
+// the cache capacity for images kept across chunked-prefill calls); the
+// pre-pass converts blocks p.img_first .. of kv_len keys and leaves the
+// earlier ones, which a previous call on the same cache prefix wrote.
 #include "bt_common.h"
 #include "bt_kernels.h"
 
@@ -48,8 +52,8 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
   static_assert(kItems <= 256, "one item per thread");
   static_assert(kPrefillKeyBlock * kDC % 256 == 0, "whole K units per thread");
   constexpr int kBlk = kPrefillKeyBlock;
-  const int blk = blockIdx.x, g = blockIdx.y;
-  const int nblk = gridDim.x;
+  const int blk = p.img_first + (int)blockIdx.x, g = blockIdx.y;
+  const int nblk = p.img_blocks;  // image layout stride per kv head
   const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(p.v + (int64_t)g * p.kv_stride_head), (short)0,
@@ -151,8 +155,10 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
 
 hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, int order, hipStream_t stream) {
   const int nblk = (p.q_offset + p.seqlen + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
-  const dim3 grid(nblk, p.kv_heads);
   if (order != kVtOrder16 && order != kVtOrder32) return hipErrorInvalidValue;
+  if (p.img_blocks < nblk || p.img_first < 0 || p.img_first > nblk) return hipErrorInvalidValue;
+  if (p.img_first == nblk) return hipSuccess;  // every block is already in the images
+  const dim3 grid(nblk - p.img_first, p.kv_heads);
   switch (head_dim) {
     case 128:
       if (order == kVtOrder16) hipLaunchKernelGGL((prefill_vts_kernel<128, kVtOrder16>), grid, dim3(256), 0, stream, p);

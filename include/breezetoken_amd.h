@@ -203,6 +203,32 @@ int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v,
                    void* out, int32_t out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
                    void* stream);
 
+/* Split-key partials bytes bt_gqa_prefill_cached uses for this shape on the
+ * current device (0: the shape runs without a split).  No reference
+ * counterpart. */
+int64_t bt_prefill_partials_bytes(int32_t seqlen, int32_t q_offset, int32_t heads, int32_t kv_heads,
+                                  int32_t head_dim);
+
+/* bt_gqa_prefill for chunked prefill over one cache, with the K / V^T images
+ * kept across calls instead of rebuilt from the whole prefix each time (the
+ * chunk loop of Qwen36MoE._attn_batch, breezetoken/model/qwen36_moe.py:
+ * 394-428, re-reads the cached prefix on every chunk).  `images` (16-byte
+ * aligned, persistent, bt_prefill_workspace_bytes(capacity, kv_heads,
+ * head_dim) bytes) holds the images laid out for `capacity` keys; the call
+ * converts the 64-key blocks from key `cached_keys` on (0 <= cached_keys <=
+ * q_offset) and trusts the earlier blocks to hold this same cache's keys from
+ * a previous call -- the prefix must not have changed since.  q_offset +
+ * seqlen <= capacity.  `partials` (may be NULL) holds the split-key partials
+ * when at least bt_prefill_partials_bytes(...) bytes.  Other arguments,
+ * results and errors as bt_gqa_prefill; the results equal bt_gqa_prefill's
+ * bit for bit. */
+int bt_gqa_prefill_cached(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,
+                          int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head, int32_t seqlen,
+                          int32_t q_offset, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
+                          void* images, int64_t images_bytes, int32_t capacity, int32_t cached_keys,
+                          void* partials, int64_t partials_bytes, void* out, int32_t out_dtype,
+                          int64_t out_stride_tok, int64_t out_stride_head, void* stream);
+
 /* Per-row RMSNorm and/or partial rotate-half RoPE over rows of f32.  Replaces
  * Backend.rms_norm (breezetoken/backends.py:44-45; torch form 187-189:
  * x * rsqrt(mean(x^2) + eps) * w) and Backend.rope (backends.py:54-62; torch

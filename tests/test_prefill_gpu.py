@@ -262,3 +262,37 @@ def test_chunked_prefill_bad_offset_raises(hip_backend):
     q, k, v, scale = _inputs(16)
     with pytest.raises(RuntimeError):
         hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, q_offset=3)
+
+
+@pytest.mark.parametrize("heads,kv,dim", [(8, 2, 256), (6, 2, 128), (16, 2, 256)])
+def test_chunked_prefill_with_kept_images_equals_fresh_images(hip_backend, heads, kv, dim):
+    """Chunked prefill over one cache with PrefillImages: every chunk converts
+    only its own blocks, and equals (bit for bit) the call that rebuilds the
+    images from the whole prefix; a rewound chunk and another cache rebuild."""
+    cap = 2048
+    g = torch.Generator().manual_seed(heads + dim)
+    k = torch.randn(cap, kv, dim, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(cap, kv, dim, generator=g).to(torch.bfloat16).cuda()
+    q_all = torch.randn(cap, heads, dim, generator=g).cuda()
+    scale = dim**-0.5
+    images = hip_backend.prefill_images(cap, kv, dim)
+    chunks = [(0, 300), (300, 401), (701, 64), (765, 1), (766, 500), (1266, 700)]
+    for pos0, s in chunks:
+        q = q_all[pos0 : pos0 + s]
+        kk, vv = k[: pos0 + s], v[: pos0 + s]
+        got = hip_backend.attention_prefill(q, kk, vv, scale, q_offset=pos0, images=images)
+        want = hip_backend.attention_prefill(q, kk, vv, scale, q_offset=pos0)
+        assert torch.equal(got, want), (pos0, s)
+        assert images.valid_keys == pos0 + s
+    # the last chunk again (cached keys only up to its own start)
+    pos0, s = chunks[-1]
+    got = hip_backend.attention_prefill(q_all[pos0 : pos0 + s], k[: pos0 + s], v[: pos0 + s], scale,
+                                        q_offset=pos0, images=images)
+    ref = orc.torch_prefill_banded(q_all[pos0 : pos0 + s].cpu(), k[: pos0 + s].float().cpu(),
+                                   v[: pos0 + s].float().cpu(), pos0, scale)
+    _close(got, ref)
+    # another cache through the same images object: rebuilt from key 0
+    k2, v2 = (k * 0.5).contiguous(), (v * 2).contiguous()
+    got = hip_backend.attention_prefill(q_all[500:600], k2[:600], v2[:600], scale, q_offset=500, images=images)
+    want = hip_backend.attention_prefill(q_all[500:600], k2[:600], v2[:600], scale, q_offset=500)
+    assert torch.equal(got, want)
