@@ -312,7 +312,14 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   const uint32_t vaddr = (uint32_t)g4 * (D * 16) + (uint32_t)i16 * 16;  // V^T: chunk g4, row dt*16 + i16
 
   // S^T = K.Q^T on the K tile kb, mask, online softmax: P^T of the step in pk.
+  // The softmax of q-tiles kNow.. is deferred to sm_tail, which runs in the
+  // P.V phase: that phase (MFMAs and V^T reads) has slack, while Q.K^T +
+  // softmax is each step's critical path.  Their masked scores wait in xd and
+  // the step's scale exponents in the *_d scalars.
+  constexpr int kNow = 1;
   u32x4 pk[NQT];
+  float xd[NQT - kNow][8];
+  int shift_d = 0, ek_d = 0, eold_d = 0, enew_d = 0;
   // Block scales (V^T and K exponents) of a step's unit, read one step ahead
   // into scalar registers so the softmax never waits for them.  Steps past this
   // group's range read the last block's (their values are unused).
@@ -321,6 +328,34 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     b64 = b64 < 0 ? 0 : (b64 < nblk64 ? b64 : nblk64 - 1);
     eb = sload(vexp, b64);
     ek = sload(kexp, b64);
+  };
+  // Online softmax of q-tile t's 32 masked scores s (keys kt*16 + g4*4 + r at
+  // s[kt*4 + r]): lazy reference max, O and l rescaled when it moves or the V
+  // scale exponent changes from e_old to e_new, P^T into pk[t].
+  auto softmax_tile = [&](int t, const float (&s)[8], int ek, int shift, int e_old, int e_new) {
+    const float c_log2 = __builtin_ldexpf(c_col[t], ek);  // log2-domain factor of the scaled scores
+    float tmax = fmax_nc(fmax_nc(fmax_nc(s[0], s[1]), fmax_nc(s[2], s[3])),
+                         fmax_nc(fmax_nc(s[4], s[5]), fmax_nc(s[6], s[7])));
+    tmax = rows16_max(tmax);
+    tmax = halves_max(tmax) * c_log2;
+    const bool move = tmax > m_ref[t] + kLazyP;
+    const float m_new = move ? tmax : m_ref[t];
+    float alpha = move ? fast_exp2(m_ref[t] - m_new) : 1.f;  // 0 when m_ref is -inf
+    m_ref[t] = m_new;
+    const float bias = (m_new == -INFINITY ? 0.f : -m_new) + (float)shift;
+    float e[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) e[r] = fast_exp2(fmaf(s[r], c_log2, bias));
+    float psum = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    if (shift != 0) psum = __builtin_ldexpf(psum, -shift);  // wave-uniform, rare
+    l_run[t] = l_run[t] * alpha + psum;
+    // Key order of the V^T chunk g4: keys g4*4 + {0..3}, 16 + g4*4 + {0..3}.
+    pk[t] = u32x4{pack_h2(e[0], e[1]), pack_h2(e[2], e[3]), pack_h2(e[4], e[5]), pack_h2(e[6], e[7])};
+    if (e_new != e_old) alpha = __builtin_ldexpf(alpha, e_old - e_new);
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max or the V scale moved
+#pragma unroll
+      for (int i = 0; i < kDTiles; ++i) oacc[t][i] *= alpha;
+    }
   };
   auto qk_sm = [&](const unsigned char* kb, int u, int eb, int ek) {
     const int blk = unit_blk(u);
@@ -375,47 +410,42 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     // takes P, i.e. the sum of P' times 2^-shift.
     const int e_new = vexp_next(e_run, eb);
     const int shift = vexp_shift(e_new, eb);
-    const float dshift = (float)shift;
 #pragma unroll
-    for (int t = 0; t < NQT; ++t) {
-      const floatx4& s0 = sacc[0][t];
-      const floatx4& s1 = sacc[1][t];
-      const float c_log2 = __builtin_ldexpf(c_col[t], ek);  // log2-domain factor of the scaled scores
-      float tmax = fmax_nc(fmax_nc(fmax_nc(s0[0], s0[1]), fmax_nc(s0[2], s0[3])),
-                           fmax_nc(fmax_nc(s1[0], s1[1]), fmax_nc(s1[2], s1[3])));
-      tmax = rows16_max(tmax);
-      tmax = halves_max(tmax) * c_log2;
-      const bool move = tmax > m_ref[t] + kLazyP;
-      const float m_new = move ? tmax : m_ref[t];
-      float alpha = move ? fast_exp2(m_ref[t] - m_new) : 1.f;  // 0 when m_ref is -inf
-      m_ref[t] = m_new;
-      const float bias = (m_new == -INFINITY ? 0.f : -m_new) + dshift;
-      float e[8];
+    for (int t = kNow; t < NQT; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        e[r] = fast_exp2(fmaf(s0[r], c_log2, bias));
-        e[4 + r] = fast_exp2(fmaf(s1[r], c_log2, bias));
+        xd[t - kNow][r] = sacc[0][t][r];
+        xd[t - kNow][4 + r] = sacc[1][t][r];
       }
-      float psum = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
-      if (shift != 0) psum = __builtin_ldexpf(psum, -shift);  // wave-uniform, rare
-      l_run[t] = l_run[t] * alpha + psum;
-      if (e_new != e_run) alpha = __builtin_ldexpf(alpha, e_run - e_new);
-      // Key order of the V^T chunk g4: keys g4*4 + {0..3}, 16 + g4*4 + {0..3}.
-      pk[t] = u32x4{pack_h2(e[0], e[1]), pack_h2(e[2], e[3]), pack_h2(e[4], e[5]), pack_h2(e[6], e[7])};
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max or the V scale moved
 #pragma unroll
-        for (int i = 0; i < kDTiles; ++i) oacc[t][i] *= alpha;
+    for (int t = 0; t < kNow; ++t) {
+      float s[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[r] = sacc[0][t][r];
+        s[4 + r] = sacc[1][t][r];
       }
+      softmax_tile(t, s, ek, shift, e_run, e_new);
     }
+    shift_d = shift;
+    ek_d = ek;
+    eold_d = e_run;
+    enew_d = e_new;
     e_run = e_new;
   };
-  // O^T += V^T.P^T on the V^T tile vb.
+  // The deferred q-tiles' softmax, row sums and P^T.
+  auto sm_tail = [&]() {
+#pragma unroll
+    for (int t = kNow; t < NQT; ++t) softmax_tile(t, xd[t - kNow], ek_d, shift_d, eold_d, enew_d);
+  };
+  // O^T += V^T.P^T on the V^T tile vb (after the step's deferred softmax).
   auto pv = [&](const unsigned char* vb) {
     auto vread = [&](int dt) -> u32x4 { return *reinterpret_cast<const u32x4*>(vb + vaddr + dt * 256); };
     constexpr int VLA = kVLead;
     u32x4 vf[VLA];
 #pragma unroll
     for (int i = 0; i < VLA; ++i) vf[i] = vread(i);
+    sm_tail();  // the first V^T reads are in flight meanwhile
 #pragma unroll
     for (int dt = 0; dt < kDTiles; ++dt) {
       const u32x4 a = vf[dt % VLA];
