@@ -16,8 +16,9 @@
 //   order kVtOrder32: key = (c/2)*16 + (c%2)*4 + {0, 1, 2, 3, 8, 9, 10, 11},
 //     the order in which a 32x32 MFMA result's registers hold P of the 16-key
 //     step c/2 for lane half c%2.
-// One thread per (chunk, 8-column slice) transposes an 8 x 8 tile in
-// registers; the block's image is assembled in LDS and stored linearly (1 KiB
+// Grid z = 0 converts K, z = 1 V (two work-groups per block, so a CU holds
+// one's loads in flight while the other converts and stores).  For V, one
+// thread per (chunk, 8-column slice) transposes an 8 x 8 tile in registers; the block's image is assembled in LDS and stored linearly (1 KiB
 // per wave instruction): 16-byte unit x sits in LDS slot x ^ ((x >> 3) & 7),
 // conflict-free both ways.
 //
@@ -64,22 +65,48 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
   __shared__ uint32_t wmax[2][4];
   const int item = threadIdx.x;
   const int c = item / kDC, dc = item % kDC;
-  // K: unit x = j * 256 + thread is slot x % kDC of row x / kDC; it holds
-  // source chunk slot ^ (row & 15).
-  constexpr int kKUnits = kBlk * kDC / 256;
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(p.k + (int64_t)g * p.kv_stride_head), (short)0,
-      (int)((uint32_t)(p.q_offset + p.seqlen) * row_bytes), 0x00020000);
-  u32x4 krow[kKUnits];
-  uint32_t kmx = 0;  // largest |k| as bf16 bits
+  if (blockIdx.z == 0) {
+    // K: unit x = j * 256 + thread is slot x % kDC of row x / kDC; it holds
+    // source chunk slot ^ (row & 15).
+    constexpr int kKUnits = kBlk * kDC / 256;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.k + (int64_t)g * p.kv_stride_head), (short)0,
+        (int)((uint32_t)(p.q_offset + p.seqlen) * row_bytes), 0x00020000);
+    u32x4 krow[kKUnits];
+    uint32_t kmx = 0;  // largest |k| as bf16 bits
 #pragma unroll
-  for (int j = 0; j < kKUnits; ++j) {
-    const int x = j * 256 + item;
-    const int r = x / kDC, slot = x % kDC;
-    krow[j] = __builtin_amdgcn_raw_buffer_load_b128(
-        krs, (int)((uint32_t)(blk * kBlk + r) * row_bytes + (uint32_t)(slot ^ (r & 15)) * 16), 0, 0);
+    for (int j = 0; j < kKUnits; ++j) {
+      const int x = j * 256 + item;
+      const int r = x / kDC, slot = x % kDC;
+      krow[j] = __builtin_amdgcn_raw_buffer_load_b128(
+          krs, (int)((uint32_t)(blk * kBlk + r) * row_bytes + (uint32_t)(slot ^ (r & 15)) * 16), 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kmx = max(kmx, max(krow[j][i] & 0x7fffu, (krow[j][i] >> 16) & 0x7fffu));
+      for (int i = 0; i < 4; ++i) kmx = max(kmx, max(krow[j][i] & 0x7fffu, (krow[j][i] >> 16) & 0x7fffu));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, o, 64));
+    if ((threadIdx.x & 63) == 0) wmax[1][threadIdx.x >> 6] = kmx;
+    __syncthreads();
+    kmx = max(max(wmax[1][0], wmax[1][1]), max(wmax[1][2], wmax[1][3]));
+    int ek = 0;
+    if (kmx != 0) {
+      const int ebits = (int)(kmx >> 7);
+      ek = (ebits == 0 ? 1 : ebits) - 127 - 14;
+    }
+    if (threadIdx.x == 0) p.kexp[g * nblk + blk] = ek;
+    uint16_t* kimg = p.kimg + ((size_t)g * nblk + blk) * kBlk * D;
+#pragma unroll
+    for (int j = 0; j < kKUnits; ++j) {
+      u32x4 o;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float f0 = __uint_as_float(krow[j][m] << 16), f1 = __uint_as_float(krow[j][m] & 0xffff0000u);
+        o[m] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                                (float2_v){__builtin_ldexpf(f0, -ek), __builtin_ldexpf(f1, -ek)}, half2_v));
+      }
+      reinterpret_cast<u32x4*>(kimg)[j * 256 + item] = o;
+    }
+    return;
   }
   u32x4 rows[8];
   uint32_t mx = 0;  // largest |v| as bf16 bits (monotonic in |v|)
@@ -94,35 +121,10 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
     }
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
-    kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, o, 64));
-  }
-  if ((threadIdx.x & 63) == 0) {
-    wmax[0][threadIdx.x >> 6] = mx;
-    wmax[1][threadIdx.x >> 6] = kmx;
-  }
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+  if ((threadIdx.x & 63) == 0) wmax[0][threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = max(max(wmax[0][0], wmax[0][1]), max(wmax[0][2], wmax[0][3]));
-  kmx = max(max(wmax[1][0], wmax[1][1]), max(wmax[1][2], wmax[1][3]));
-  int ek = 0;
-  if (kmx != 0) {
-    const int ebits = (int)(kmx >> 7);
-    ek = (ebits == 0 ? 1 : ebits) - 127 - 14;
-  }
-  if (threadIdx.x == 0) p.kexp[g * nblk + blk] = ek;
-  uint16_t* kimg = p.kimg + ((size_t)g * nblk + blk) * kBlk * D;
-#pragma unroll
-  for (int j = 0; j < kKUnits; ++j) {
-    u32x4 o;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const float f0 = __uint_as_float(krow[j][m] << 16), f1 = __uint_as_float(krow[j][m] & 0xffff0000u);
-      o[m] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
-                                              (float2_v){__builtin_ldexpf(f0, -ek), __builtin_ldexpf(f1, -ek)}, half2_v));
-    }
-    reinterpret_cast<u32x4*>(kimg)[j * 256 + item] = o;
-  }
   int e = kVExpZero;
   if (mx != 0) {
     const int ebits = (int)(mx >> 7);                 // biased exponent (0: subnormal)
@@ -158,7 +160,7 @@ hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, int order, h
   if (order != kVtOrder16 && order != kVtOrder32) return hipErrorInvalidValue;
   if (p.img_blocks < nblk || p.img_first < 0 || p.img_first > nblk) return hipErrorInvalidValue;
   if (p.img_first == nblk) return hipSuccess;  // every block is already in the images
-  const dim3 grid(nblk - p.img_first, p.kv_heads);
+  const dim3 grid(nblk - p.img_first, p.kv_heads, 2);
   switch (head_dim) {
     case 128:
       if (order == kVtOrder16) hipLaunchKernelGGL((prefill_vts_kernel<128, kVtOrder16>), grid, dim3(256), 0, stream, p);
