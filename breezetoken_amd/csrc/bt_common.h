@@ -130,24 +130,6 @@ __device__ __forceinline__ int vexp_shift(int e_new, int eb) { return eb == kVEx
 
 // Prefill queries enter Q.K^T as fp16 scaled by 2^-e per query row (f32 or
 // bf16 q alike), e = E - 14 for the row's largest |q| (0 for a row of zeros).
-// Largest |q| of the 8 values at q + off (f32 or bf16 elements) as f32 bits,
-// which order like |q|.
-__device__ __forceinline__ uint32_t q_chunk_absmax(const void* q, bool f32, int64_t off) {
-  uint32_t mx = 0;
-  if (f32) {
-    const float* qf = reinterpret_cast<const float*>(q) + off;
-    const float4 a = *reinterpret_cast<const float4*>(qf);
-    const float4 b = *reinterpret_cast<const float4*>(qf + 4);
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) mx = max(mx, __float_as_uint(v[i]) & 0x7fffffffu);
-  } else {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(q) + off);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx = max(mx, max((w[i] << 16) & 0x7fffffffu, w[i] & 0x7fff0000u));
-  }
-  return mx;
-}
 __device__ __forceinline__ int absmax_exp(uint32_t bits) {
   if (bits == 0) return 0;
   const int ebits = (int)(bits >> 23);
@@ -159,24 +141,57 @@ __device__ __forceinline__ uint32_t pack_f16x2_scaled(float a, float b, int e) {
   return __builtin_bit_cast(uint32_t,
                             __builtin_convertvector((float2_c){__builtin_ldexpf(a, -e), __builtin_ldexpf(b, -e)}, half2_c));
 }
-// The 8 values at q + off times 2^-e as an fp16 MFMA operand (round to nearest even).
-__device__ __forceinline__ u32x4 q_chunk_f16(const void* q, bool f32, int64_t off, int e) {
-  float v[8];
+// One query row's N chunks of 8 values (chunk i at q + off + i * step
+// elements, f32 or bf16) as fp16 MFMA operands scaled by 2^-e, e from the
+// row's largest |q|.  Every load is issued before any is used, so the row
+// costs one memory round trip; `reduce` combines the maxima (as f32 bits of
+// |q|, which order like |q|) of the lanes that share the row.  Returns e.
+template <int N, typename Reduce>
+__device__ __forceinline__ int q_row_f16(const void* q, bool f32, int64_t off, int step, u32x4 (&out)[N],
+                                         Reduce reduce) {
+  uint32_t mx = 0;
   if (f32) {
     const float* qf = reinterpret_cast<const float*>(q) + off;
-    const float4 a = *reinterpret_cast<const float4*>(qf);
-    const float4 b = *reinterpret_cast<const float4*>(qf + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(q) + off);
+    float4 raw[N][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(w[i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    for (int i = 0; i < N; ++i) {
+      raw[i][0] = *reinterpret_cast<const float4*>(qf + (int64_t)i * step);
+      raw[i][1] = *reinterpret_cast<const float4*>(qf + (int64_t)i * step + 4);
     }
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 v = raw[i][h];
+        mx = max(mx, max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
+                         max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu)));
+      }
+    const int e = absmax_exp(reduce(mx));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const float4 a = raw[i][0], b = raw[i][1];
+      out[i] = u32x4{pack_f16x2_scaled(a.x, a.y, e), pack_f16x2_scaled(a.z, a.w, e), pack_f16x2_scaled(b.x, b.y, e),
+                     pack_f16x2_scaled(b.z, b.w, e)};
+    }
+    return e;
   }
-  return u32x4{pack_f16x2_scaled(v[0], v[1], e), pack_f16x2_scaled(v[2], v[3], e),
-               pack_f16x2_scaled(v[4], v[5], e), pack_f16x2_scaled(v[6], v[7], e)};
+  const uint16_t* qb = reinterpret_cast<const uint16_t*>(q) + off;
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = *reinterpret_cast<const u32x4*>(qb + (int64_t)i * step);
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = max(mx, max((out[i][j] << 16) & 0x7fffffffu, out[i][j] & 0x7fff0000u));
+  const int e = absmax_exp(reduce(mx));
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const u32x4 w = out[i];
+    out[i] = u32x4{pack_f16x2_scaled(__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u), e),
+                   pack_f16x2_scaled(__uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u), e),
+                   pack_f16x2_scaled(__uint_as_float(w[2] << 16), __uint_as_float(w[2] & 0xffff0000u), e),
+                   pack_f16x2_scaled(__uint_as_float(w[3] << 16), __uint_as_float(w[3] & 0xffff0000u), e)};
+  }
+  return e;
 }
 
 }  // namespace bt

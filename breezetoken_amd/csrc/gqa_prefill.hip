@@ -214,15 +214,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     {
       const int qrow = min(q0 + qcol, S - 1);
       const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + kgrp * 8;
-      const bool f32 = p.q_f32 != 0;
-      uint32_t mx = 0;
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) mx = max(mx, q_chunk_absmax(p.q, f32, off + st * 16));
-      mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));  // the row's two lane halves
-      const int eq = absmax_exp(mx);
+      const int eq = q_row_f16(p.q, p.q_f32 != 0, off, 16, qop, [](uint32_t mx) {
+        return max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));  // the row's two lane halves
+      });
       c_col = __builtin_ldexpf(p.scale_log2, eq);
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) qop[st] = q_chunk_f16(p.q, f32, off + st * 16, eq);
     }
     float c_blk = c_col;  // log2-domain factor of the latest block's scaled scores
 
@@ -305,20 +300,19 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     // 32..63 follow in softmax_tail beside the next block's S = K.Q^T.  The
     // V^T block's power-of-two scale enters P' = P * 2^shift through the exp2
     // bias; the row sum takes P.
-    auto softmax_head = [&](int kb, floatx16(&sacc)[2], uint32_t(&out)[8]) -> float {
+    auto softmax_head = [&](floatx16(&sacc)[2], uint32_t(&out)[8], int ek, int eb) -> float {
       float tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int j = 0; j < 16; ++j) tmax = fmaxf(tmax, sacc[mt][j]);
-      c_blk = __builtin_ldexpf(c_col, sload(kexp, kb));  // with the K block's scale
+      c_blk = __builtin_ldexpf(c_col, ek);  // with the K block's scale
       tmax = halves_max(tmax) * c_blk;
       // lazy reference max: move it only when a score exceeds it by > kLazy
       const bool move = tmax > m_ref + kLazy;
       const float m_new = move ? tmax : m_ref;
       const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
       m_ref = m_new;
-      const int eb = sload(vexp, kb);
       const int e_new = vexp_next(e_run, eb);
       tail_shift = vexp_shift(e_new, eb);
       neg_m_tail = (m_ref == -INFINITY ? 0.f : -m_ref) + (float)tail_shift;
@@ -352,6 +346,15 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     //   end barrier of step kb: K_{kb+1} has landed (likewise)
     // Copies past the last block re-read the last block (min(., last)) into a
     // buffer nobody reads, so the key loop has no branches around its copies.
+    // Block scale exponents (K, V^T) of the block being softmaxed, read
+    // through the scalar cache a block ahead of their use.
+    auto scales = [&](int kb, int& ek, int& eb) {
+      const int b = min(kb, last);
+      ek = sload(kexp, b);
+      eb = sload(vexp, b);
+    };
+    int ek_c, eb_c;
+    scales(0, ek_c, eb_c);
     copy_k(Buf<0>{}, 0);
     copy_k(Buf<1>{}, min(1, last));
     copy_v(Buf<0>{}, 0);
@@ -365,7 +368,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       barrier();  // every wave is done reading K_0
       copy_k(Buf<0>{}, min(2, last));
       if (0 >= kb_diag) mask(0, sacc);
-      rescale(softmax_head(0, sacc, pk0));
+      int ek_n, eb_n;
+      scales(1, ek_n, eb_n);
+      rescale(softmax_head(sacc, pk0, ek_c, eb_c));
+      ek_c = ek_n;
+      eb_c = eb_n;
       barrier();  // K_1 landed in the prologue
     }
     // Block kb (buffer b = kb % 2), two matrix-core phases with VALU work
@@ -375,6 +382,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     auto step = [&](auto b, int kb) {
       constexpr int B = decltype(b)::value;
       copy_v(b, kb);
+      int ek_n, eb_n;
+      scales(kb + 1, ek_n, eb_n);
       floatx16 sacc[2];
       qk(b, sacc);
       softmax_tail();
@@ -385,7 +394,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       if (kb >= kb_diag) mask(kb, sacc);
       pv(Buf<B ^ 1>{}, pk0, pk1);
       uint32_t pk0_next[8];
-      const float alpha = softmax_head(kb, sacc, pk0_next);
+      const float alpha = softmax_head(sacc, pk0_next, ek_c, eb_c);
+      ek_c = ek_n;
+      eb_c = eb_n;
       interleave<kDTiles * 4, 4, 4, kCopies>();
       rescale(alpha);
 #pragma unroll

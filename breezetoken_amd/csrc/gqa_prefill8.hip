@@ -166,21 +166,27 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   // Q^T operand: lane holds Q[q0 + i16][st*32 + g4*8 .. +8] for each 32-d step
   // as fp16, the row scaled by 2^-eq so its largest |q| lies in [2^14, 2^15);
   // c_col = scale * log2(e) * 2^eq restores it in the exp2 argument.
+  // K and V^T scale exponents of a block, read through the scalar cache a
+  // block ahead of their use (each read is a dependent round trip to memory
+  // the pre-pass just wrote).
+  const int* vexp = p.vexp + kvh * p.img_blocks;
+  auto scales = [&](int kb, int& ek, int& eb) {
+    const int b = min(kb, last);
+    ek = sload(kexp, b);
+    eb = sload(vexp, b);
+  };
+  int ek_c, eb_c;
+  scales(kb0, ek_c, eb_c);
   u32x4 qop[kDSteps];
   float c_col;
   {
     const int qrow = min(q0 + i16, S - 1);
     const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + g4 * 8;
-    const bool f32 = p.q_f32 != 0;
-    uint32_t mx = 0;
-#pragma unroll
-    for (int st = 0; st < kDSteps; ++st) mx = max(mx, q_chunk_absmax(p.q, f32, off + st * 32));
-    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
-    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
-    const int eq = absmax_exp(mx);
+    const int eq = q_row_f16(p.q, p.q_f32 != 0, off, 32, qop, [](uint32_t mx) {
+      mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
+      return max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+    });
     c_col = __builtin_ldexpf(p.scale_log2, eq);
-#pragma unroll
-    for (int st = 0; st < kDSteps; ++st) qop[st] = q_chunk_f16(p.q, f32, off + st * 32, eq);
   }
 
   floatx4 oacc[kDTiles];
@@ -189,7 +195,6 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   float m_ref = -INFINITY;          // reference max (log2 domain) of this lane's query column
   float l_run = 0.f;                // partial row sum over this lane's keys
   int e_run = kVExpZero;            // V scale O is kept in: O_true = O * 2^e_run
-  const int* vexp = p.vexp + kvh * p.img_blocks;
   const int my_q = q0 + i16;
   const int my_pos = P0 + my_q;     // keys 0 .. my_pos
   u32x4 pk[2];                      // P of the pending block: 32-key halves, fp16
@@ -239,20 +244,19 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   // P as fp16 in the MFMA key order; returns the factor O must be scaled by.
   // The V^T block's power-of-two scale enters P' = P * 2^shift through the
   // exp2 bias; the row sum takes P.
-  auto softmax = [&](int kb, floatx4 (&sacc)[4], u32x4 (&out)[2]) -> float {
+  auto softmax = [&](floatx4 (&sacc)[4], u32x4 (&out)[2], int ek, int eb) -> float {
     float tmax = -INFINITY;
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
       for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[sub][r]);
-    const float c_log2 = __builtin_ldexpf(c_col, sload(kexp, kb));  // with the K block's scale
+    const float c_log2 = __builtin_ldexpf(c_col, ek);  // with the K block's scale
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = halves_max(tmax) * c_log2;
     const bool move = tmax > m_ref + kLazy8;
     const float m_new = move ? tmax : m_ref;
     const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
     m_ref = m_new;
-    const int eb = sload(vexp, kb);
     const int e_new = vexp_next(e_run, eb);
     const int shift = vexp_shift(e_new, eb);
     const float neg_m = (m_ref == -INFINITY ? 0.f : -m_ref) + (float)shift;
@@ -298,7 +302,11 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     barrier();
     copy_k(Buf8<0>{}, min(kb0 + 2, last));
     if (kb0 >= kb_diag) mask(kb0, sacc);
-    softmax(kb0, sacc, pk);  // O is still zero: its factor does not matter
+    int ek_n, eb_n;
+    scales(kb0 + 1, ek_n, eb_n);
+    softmax(sacc, pk, ek_c, eb_c);  // O is still zero: its factor does not matter
+    ek_c = ek_n;
+    eb_c = eb_n;
     barrier();
   }
   // Block kb: A: S_kb = K_kb . Q^T; B: O += V_{kb-1} . P_{kb-1} beside the
@@ -306,6 +314,8 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   auto step = [&](auto b, int kb) {
     constexpr int B = decltype(b)::value;
     copy_v(b, kb);
+    int ek_n, eb_n;
+    scales(kb + 1, ek_n, eb_n);
     floatx4 sacc[4];
     qk(b, sacc);
     wait_older();  // V_{kb-1}
@@ -314,7 +324,9 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     if (kb >= kb_diag) mask(kb, sacc);
     pv(Buf8<B ^ 1>{}, pk);
     u32x4 pk_next[2];
-    const float alpha = softmax(kb, sacc, pk_next);
+    const float alpha = softmax(sacc, pk_next, ek_c, eb_c);
+    ek_c = ek_n;
+    eb_c = eb_n;
     rescale(alpha);
     pk[0] = pk_next[0];
     pk[1] = pk_next[1];
