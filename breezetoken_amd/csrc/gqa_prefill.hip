@@ -205,6 +205,19 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     // masked like any causal key, so no branch is needed inside the key loop.
     const bool wave_active = wave < GW * (kWaves / GW) && head_local < G && q0 < S;
     const int head = kvh * G + min(head_local, G - 1);
+    // Block scale exponents (K, V^T) of the block being softmaxed, read
+    // through the scalar cache a block ahead of their use.
+    auto scales = [&](int kb, int& ek, int& eb) {
+      const int b = min(kb, last);
+      ek = sload(kexp, b);
+      eb = sload(vexp, b);
+    };
+    int ek_c, eb_c;
+    scales(0, ek_c, eb_c);
+    // The first tiles go out before the q loads, so the two latencies overlap.
+    copy_k(Buf<0>{}, 0);
+    copy_k(Buf<1>{}, min(1, last));
+    copy_v(Buf<0>{}, 0);
 
     // ---- Q^T operand in registers: lane holds Q[q0 + qcol][d = st*16 + kgrp*8 .. +8]
     // as fp16, the row scaled by 2^-eq so its largest |q| lies in [2^14,
@@ -346,18 +359,6 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
     //   end barrier of step kb: K_{kb+1} has landed (likewise)
     // Copies past the last block re-read the last block (min(., last)) into a
     // buffer nobody reads, so the key loop has no branches around its copies.
-    // Block scale exponents (K, V^T) of the block being softmaxed, read
-    // through the scalar cache a block ahead of their use.
-    auto scales = [&](int kb, int& ek, int& eb) {
-      const int b = min(kb, last);
-      ek = sload(kexp, b);
-      eb = sload(vexp, b);
-    };
-    int ek_c, eb_c;
-    scales(0, ek_c, eb_c);
-    copy_k(Buf<0>{}, 0);
-    copy_k(Buf<1>{}, min(1, last));
-    copy_v(Buf<0>{}, 0);
     wait_all();
     __syncthreads();
 

@@ -150,12 +150,16 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     }
   };
   // Each wave waits for its own copies; the barrier that follows publishes
-  // them.  wait_all: vmcnt(0); wait_older: all but the 2 * kCopies youngest.
+  // them.  vmcnt counts a wave's loads in issue order, so naming how many
+  // tiles (kCopies loads each) were issued after the awaited one waits for
+  // exactly that tile and the older ones.
   auto wait_all = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };
-  constexpr int kYoung = 2 * kCopies;
-  constexpr int kWaitOlder = 0x0f70 | (kYoung & 0xf) | ((kYoung >> 4) << 14);
-  static_assert(kYoung < 64, "vmcnt holds 6 bits");
-  auto wait_older = [] { __builtin_amdgcn_s_waitcnt(kWaitOlder); };
+  static_assert(2 * kCopies < 64, "vmcnt holds 6 bits");
+  auto wait_tiles = [](int younger) {
+    if (younger >= 2) __builtin_amdgcn_s_waitcnt(0x0f70 | ((2 * kCopies) & 0xf) | (((2 * kCopies) >> 4) << 14));
+    else if (younger == 1) __builtin_amdgcn_s_waitcnt(0x0f70 | (kCopies & 0xf) | ((kCopies >> 4) << 14));
+    else __builtin_amdgcn_s_waitcnt(0x0f70);
+  };
   // Work-group barrier without __syncthreads' fence (which would wait for
   // every copy in flight); the LDS reads before it were consumed by MFMAs.
   auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
@@ -177,6 +181,18 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   };
   int ek_c, eb_c;
   scales(kb0, ek_c, eb_c);
+  // Copy schedule (as in the one-wave kernel):
+  //   start of step kb: V_kb -> V buffer kb % 2; after the mid barrier: K_{kb+2}
+  //   -> K buffer kb % 2; the mid barrier publishes V_{kb-1}, the end barrier
+  //   K_{kb+1}.  No copy goes past the last block (a short work-group would
+  //   otherwise wait for them at its end).
+  // Buffers alternate from the work-group's first block kb0.  The first tiles,
+  // and V_{kb0+1} (which the generic schedule would issue a step later), go out
+  // before the q loads, so their latencies overlap.
+  copy_k(Buf8<0>{}, kb0);
+  if (kb0 + 1 <= last) copy_k(Buf8<1>{}, kb0 + 1);
+  copy_v(Buf8<0>{}, kb0);
+  if (kb0 + 1 <= last) copy_v(Buf8<1>{}, kb0 + 1);
   u32x4 qop[kDSteps];
   float c_col;
   {
@@ -286,21 +302,13 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   };
   const int kb_diag = (P0 + q0 + 1) / kKB8;  // earlier blocks need no mask
 
-  // Copy schedule (as in the one-wave kernel):
-  //   start of step kb: V_kb -> V buffer kb % 2; after the mid barrier: K_{kb+2}
-  //   -> K buffer kb % 2; the mid barrier publishes V_{kb-1}, the end barrier
-  //   K_{kb+1}.  Copies past the last block re-read the last block.
-  // Buffers alternate from the work-group's first block kb0.
-  copy_k(Buf8<0>{}, kb0);
-  copy_k(Buf8<1>{}, min(kb0 + 1, last));
-  copy_v(Buf8<0>{}, kb0);
   wait_all();
   __syncthreads();
   {
     floatx4 sacc[4];
     qk(Buf8<0>{}, sacc);
     barrier();
-    copy_k(Buf8<0>{}, min(kb0 + 2, last));
+    if (kb0 + 2 <= last) copy_k(Buf8<0>{}, kb0 + 2);
     if (kb0 >= kb_diag) mask(kb0, sacc);
     int ek_n, eb_n;
     scales(kb0 + 1, ek_n, eb_n);
@@ -313,14 +321,17 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   // softmax of S_kb.
   auto step = [&](auto b, int kb) {
     constexpr int B = decltype(b)::value;
-    copy_v(b, kb);
+    const bool second = kb == kb0 + 1;  // its V^T went out in the prologue
+    if (!second) copy_v(b, kb);
     int ek_n, eb_n;
     scales(kb + 1, ek_n, eb_n);
     floatx4 sacc[4];
     qk(b, sacc);
-    wait_older();  // V_{kb-1}
+    // V_{kb-1}; issued after it: K_{kb+1} (if any) and V_kb (in the second
+    // block: V_{kb0+1}, from the prologue).
+    wait_tiles((kb + 1 <= last ? 1 : 0) + 1);
     barrier();
-    copy_k(b, min(kb + 2, last));
+    if (kb + 2 <= last) copy_k(b, kb + 2);
     if (kb >= kb_diag) mask(kb, sacc);
     pv(Buf8<B ^ 1>{}, pk);
     u32x4 pk_next[2];
@@ -330,7 +341,9 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     rescale(alpha);
     pk[0] = pk_next[0];
     pk[1] = pk_next[1];
-    wait_older();  // K_{kb+1}
+    // K_{kb+1} (if any); issued after it: V_kb (except in the second block,
+    // whose V^T went out in the prologue) and K_{kb+2} (if any).
+    wait_tiles((second ? 0 : 1) + (kb + 2 <= last ? 1 : 0));
     barrier();
   };
   // Every pass of the loop ends with a buffer-0 step, so no path reaches the

@@ -472,12 +472,13 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     else __builtin_amdgcn_s_waitcnt(0x0f70);
   };
 
-  int cur_blk = unit_blk(first);
-  load_q(cur_blk);
-  reset();
+  // The first tiles go out before the q loads, so the two latencies overlap.
   if (first < my_steps) {
     if (first & 1) { copy_k(K1, first); copy_v(V1, first); } else { copy_k(K0, first); copy_v(V0, first); }
   }
+  int cur_blk = unit_blk(first);
+  load_q(cur_blk);
+  reset();
   auto working = [&](int st) { return st >= first && st < my_steps; };
   // Each step has two barrier phases.  The two groups put their MFMA-heavy
   // and VALU-heavy work in opposite phases, so the two waves that share a
