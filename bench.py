@@ -191,15 +191,18 @@ def cpu_baselines(torch, head_case, L: int, nbytes: int, seconds: float, headlin
     return head, rows
 
 
-def prefill_mode(torch, backend, dev, calls: int, q_f32: bool = False) -> int:
+def prefill_mode(torch, backend, dev, calls: int, q_f32: bool = False, warmup: int = 2) -> int:
     """Config-4 prefill at S=8192 only (for rocprofv3 kernel traces): ``calls``
-    calls after two warm-up calls, timed with HIP events on the current stream.
-    q is bf16 as config 4 draws it, or its f32 draws (``q_f32``)."""
+    calls after ``warmup`` warm-up calls, timed with HIP events on the current
+    stream.  q is bf16 as config 4 draws it, or its f32 draws (``q_f32``).
+    MFMA-heavy work runs ~10% slower for its first ~10 ms in a process (clock
+    ramp), so a trace meant to match the warmed bench number wants ~50
+    warm-up calls."""
     from breezetoken_amd import workloads as wl
 
     q, k, v, scale = wl.c4_inputs(8192, q_f32=q_f32)
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
-    for _ in range(2):
+    for _ in range(max(0, warmup)):
         backend.attention_prefill(q, k, v, scale, torch.bfloat16)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -355,7 +358,7 @@ def main() -> int:
     if args.mode == "pmc":
         return pmc_mode(torch, backend, dev)
     if args.mode == "prefill":
-        return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)), args.q_f32)
+        return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)), args.q_f32, min(args.warmup, 200))
     if args.mode == "decode":
         return decode_mode(torch, backend, dev, max(1, min(args.steps, 2000)), args.valid)
     if args.mode == "ragged":
