@@ -78,6 +78,7 @@ struct PrefillParams {
   int32_t img_blocks;  // 64-key blocks per kv head in the image layout (>= those of q_offset + seqlen keys)
   int32_t img_first;   // first block the pre-pass converts (the images already hold the earlier ones)
   int32_t q_f32;       // 1: q is f32, 0: bf16 (either enters Q.K^T as fp16 scaled per row)
+  int32_t keep_images; // 1: the images must hold every block afterwards (kept across chunked-prefill calls)
   // Split-key mode of the two-waves-per-SIMD kernel (kb_chunk > 0): work-group
   // (query block, kv head, chunk c) covers key blocks [c*kb_chunk, +kb_chunk);
   // a query block with more than one chunk writes one normalised partial and

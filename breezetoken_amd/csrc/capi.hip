@@ -458,9 +458,9 @@ int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32
 static int prefill_run(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,
                        int64_t q_stride_head, int64_t kv_stride_tok, int64_t kv_stride_head, int32_t seqlen,
                        int32_t q_offset, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
-                       void* images, int32_t img_keys, int32_t img_first_key, void* partials,
-                       int64_t partials_bytes, void* out, int32_t out_dtype, int64_t out_stride_tok,
-                       int64_t out_stride_head, void* stream) {
+                       void* images, int32_t img_keys, int32_t img_first_key, bool keep_images,
+                       void* partials, int64_t partials_bytes, void* out, int32_t out_dtype,
+                       int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
   if (!q || !k || !v || !out || !images) return BT_EINVAL;
   if (seqlen < 1 || q_offset < 0 || heads < 1 || kv_heads < 1 || heads % kv_heads) return BT_EINVAL;
   if ((int64_t)q_offset + seqlen > INT32_MAX) return BT_EINVAL;
@@ -511,6 +511,7 @@ static int prefill_run(const void* q, int32_t q_dtype, const void* k, const void
   p.img_blocks = (int32_t)img_blocks;
   p.img_first = img_first_key / bt::kPrefillKeyBlock;
   p.q_f32 = q_dtype == BT_DTYPE_F32 ? 1 : 0;
+  p.keep_images = keep_images ? 1 : 0;
   if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim))
     return hip_rc(bt::launch_prefill_pair(p, head_dim, (hipStream_t)stream));
   // Group sizes 1, 2, 4, 8 at D = 128 / 256 run two waves per SIMD; other
@@ -546,7 +547,7 @@ int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v,
   const int64_t part_offset = align256(prefill_base_bytes(kv_len, kv_heads, head_dim));
   void* partials = workspace_bytes > part_offset ? static_cast<char*>(workspace) + part_offset : nullptr;
   return prefill_run(q, q_dtype, k, v, q_stride_tok, q_stride_head, kv_stride_tok, kv_stride_head, seqlen,
-                     q_offset, heads, kv_heads, head_dim, scale, workspace, kv_len, 0, partials,
+                     q_offset, heads, kv_heads, head_dim, scale, workspace, kv_len, 0, false, partials,
                      partials ? workspace_bytes - part_offset : 0, out, out_dtype, out_stride_tok,
                      out_stride_head, stream);
 }
@@ -570,8 +571,8 @@ int bt_gqa_prefill_cached(const void* q, int32_t q_dtype, const void* k, const v
   if (cached_keys < 0 || cached_keys > q_offset) return BT_EINVAL;
   if (images_bytes < bt_prefill_workspace_bytes(capacity, kv_heads, head_dim)) return BT_ENOSPC;
   return prefill_run(q, q_dtype, k, v, q_stride_tok, q_stride_head, kv_stride_tok, kv_stride_head, seqlen,
-                     q_offset, heads, kv_heads, head_dim, scale, images, capacity, cached_keys, partials,
-                     partials_bytes, out, out_dtype, out_stride_tok, out_stride_head, stream);
+                     q_offset, heads, kv_heads, head_dim, scale, images, capacity, cached_keys, true,
+                     partials, partials_bytes, out, out_dtype, out_stride_tok, out_stride_head, stream);
 }
 
 static bool prep_dim_served(int32_t d) { return d == 64 || d == 128 || d == 256 || d == 512; }

@@ -76,7 +76,11 @@ __device__ __forceinline__ uint32_t pack_rne8(float a, float b) {
 
 }  // namespace
 
-template <int D>
+// DIRECT: a work-group with at most two key blocks converts them from the bf16
+// cache straight into its LDS tiles (the layout and rounding of the images
+// of gqa_prefill_vt.hip, same block scales), so a short prompt needs no
+// pre-pass launch.
+template <int D, bool DIRECT>
 __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillParams p) {
   constexpr int kDSteps = D / 32;      // K-dimension steps of Q.K^T (32 per MFMA)
   constexpr int kDTiles = D / 16;      // 16-row d tiles of O^T
@@ -90,6 +94,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[kImg];
   __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kImg];
   __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[kImg];
+  __shared__ uint32_t dmax[2][kWaves8];  // DIRECT: per-wave block maxima
   auto k_buf = [&](auto b) -> unsigned char* {
     if constexpr (decltype(b)::value == 0) return k_lds0; else return k_lds1;
   };
@@ -174,13 +179,18 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   // block ahead of their use (each read is a dependent round trip to memory
   // the pre-pass just wrote).
   const int* vexp = p.vexp + kvh * p.img_blocks;
+  int dek[2] = {0, 0}, deb[2] = {kVExpZero, kVExpZero};  // DIRECT: exponents of blocks kb0, kb0 + 1
   auto scales = [&](int kb, int& ek, int& eb) {
-    const int b = min(kb, last);
-    ek = sload(kexp, b);
-    eb = sload(vexp, b);
+    if constexpr (DIRECT) {
+      const bool second = min(kb, last) > kb0;
+      ek = second ? dek[1] : dek[0];
+      eb = second ? deb[1] : deb[0];
+    } else {
+      const int b = min(kb, last);
+      ek = sload(kexp, b);
+      eb = sload(vexp, b);
+    }
   };
-  int ek_c, eb_c;
-  scales(kb0, ek_c, eb_c);
   // Copy schedule (as in the one-wave kernel):
   //   start of step kb: V_kb -> V buffer kb % 2; after the mid barrier: K_{kb+2}
   //   -> K buffer kb % 2; the mid barrier publishes V_{kb-1}, the end barrier
@@ -189,10 +199,48 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   // Buffers alternate from the work-group's first block kb0.  The first tiles,
   // and V_{kb0+1} (which the generic schedule would issue a step later), go out
   // before the q loads, so their latencies overlap.
-  copy_k(Buf8<0>{}, kb0);
-  if (kb0 + 1 <= last) copy_k(Buf8<1>{}, kb0 + 1);
-  copy_v(Buf8<0>{}, kb0);
-  if (kb0 + 1 <= last) copy_v(Buf8<1>{}, kb0 + 1);
+  // DIRECT: threads 0..255 hold V items (chunk c, 8-column slice dc: the 8
+  // keys of chunk c at those columns), threads 256..511 K units (16-byte slot
+  // of a key row), for both blocks; loads go out before the q loads.
+  constexpr int kDC = D / 8;                 // 16-byte column chunks per row
+  constexpr int kVItems = 8 * kDC;           // V^T items per block
+  constexpr int kKPer = kKB8 * kDC / 256;    // K units per K thread per block
+  static_assert(kVItems <= 256 && kKPer >= 1, "head_dim 128 or 256");
+  u32x4 draw[2][8];
+  if constexpr (DIRECT) {
+    const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+    const uint32_t range = (uint32_t)nkeys * row_bytes;  // keys past the prompt read as zero
+    if (t < 256) {
+      const __amdgpu_buffer_rsrc_t vsrc = rsrc8(p.v + (int64_t)kvh * p.kv_stride_head, range);
+      const int c = t / kDC, dc = t % kDC;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        if (t < kVItems && kb0 + b <= last)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int key = (kb0 + b) * kKB8 + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16;
+            draw[b][j] = load16_8(vsrc, (uint32_t)key * row_bytes + (uint32_t)dc * 16);
+          }
+    } else {
+      const __amdgpu_buffer_rsrc_t ksrc = rsrc8(p.k + (int64_t)kvh * p.kv_stride_head, range);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        if (kb0 + b <= last)
+#pragma unroll
+          for (int j = 0; j < kKPer; ++j) {
+            const int x = j * 256 + (t - 256);
+            const int r = x / kDC, slot = x % kDC;
+            draw[b][j] = load16_8(ksrc, (uint32_t)((kb0 + b) * kKB8 + r) * row_bytes + (uint32_t)(slot ^ (r & 15)) * 16);
+          }
+    }
+  } else {
+    copy_k(Buf8<0>{}, kb0);
+    if (kb0 + 1 <= last) copy_k(Buf8<1>{}, kb0 + 1);
+    copy_v(Buf8<0>{}, kb0);
+    if (kb0 + 1 <= last) copy_v(Buf8<1>{}, kb0 + 1);
+  }
+  int ek_c, eb_c;
+  if constexpr (!DIRECT) scales(kb0, ek_c, eb_c);
   u32x4 qop[kDSteps];
   float c_col;
   {
@@ -203,6 +251,79 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       return max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
     });
     c_col = __builtin_ldexpf(p.scale_log2, eq);
+  }
+  if constexpr (DIRECT) {
+    // Block maxima (bf16 bits of |x|, which order like |x|): V over waves
+    // 0..3, K over waves 4..7; then every thread derives the same exponents.
+    uint32_t mx[2] = {0u, 0u};
+    const int nj = t < 256 ? (t < kVItems ? 8 : 0) : kKPer;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+      if (kb0 + b <= last)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (j < nj)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              mx[b] = max(mx[b], max(draw[b][j][i] & 0x7fffu, (draw[b][j][i] >> 16) & 0x7fffu));
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx[b] = max(mx[b], (uint32_t)__shfl_xor((int)mx[b], o, 64));
+      if (lane == 0) dmax[b][wave] = mx[b];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const uint32_t vm = max(max(dmax[b][0], dmax[b][1]), max(dmax[b][2], dmax[b][3]));
+      const uint32_t km = max(max(dmax[b][4], dmax[b][5]), max(dmax[b][6], dmax[b][7]));
+      if (km != 0) {
+        const int ebits = (int)(km >> 7);
+        dek[b] = (ebits == 0 ? 1 : ebits) - 127 - 14;
+      }
+      if (vm != 0) {
+        const int ebits = (int)(vm >> 7);
+        const int E = (ebits == 0 ? 1 : ebits) - 127;
+        deb[b] = E <= 14 ? -4 * ((14 - E) / 4) : 4 * ((E - 14 + 3) / 4);  // 4 * ceil((E - 14) / 4)
+      }
+    }
+    auto to_f16 = [](float a, float b, int e) {
+      return __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                              (float2v_8){__builtin_ldexpf(a, -e), __builtin_ldexpf(b, -e)}, half2v_8));
+    };
+    auto write_tiles = [&](auto bsel) {
+      constexpr int b = decltype(bsel)::value;
+      if (kb0 + b > last) return;
+      if (t < 256) {
+        if (t >= kVItems) return;
+        const int c = t / kDC, dc = t % kDC;
+        const int e = deb[b];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // V^T row d = dc*8 + i of chunk c
+          u32x4 o;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const uint32_t w0 = draw[b][2 * m][i >> 1], w1 = draw[b][2 * m + 1][i >> 1];
+            o[m] = to_f16(__uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16)),
+                          __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16)), e);
+          }
+          *reinterpret_cast<u32x4*>(v_buf(bsel) + (c * D + dc * 8 + i) * 16) = o;
+        }
+      } else {
+        const int e = dek[b];
+#pragma unroll
+        for (int j = 0; j < kKPer; ++j) {  // unit x lands at x * 16: row x / kDC, slot x % kDC
+          u32x4 o;
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            o[m] = to_f16(__uint_as_float(draw[b][j][m] << 16), __uint_as_float(draw[b][j][m] & 0xffff0000u), e);
+          *reinterpret_cast<u32x4*>(k_buf(bsel) + (j * 256 + (t - 256)) * 16) = o;
+        }
+      }
+    };
+    write_tiles(Buf8<0>{});
+    write_tiles(Buf8<1>{});
+    scales(kb0, ek_c, eb_c);
   }
 
   floatx4 oacc[kDTiles];
@@ -520,15 +641,23 @@ hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t str
   if (split && (p.max_chunks < 1 || p.max_chunks > kMaxChunks || !p.part || !p.lse)) return hipErrorInvalidValue;
   const dim3 grid(nqb, p.kv_heads, split ? p.max_chunks : 1);
   const dim3 cgrid(nqb, p.kv_heads, kRows8 * head_dim / 4 / 256);
-  const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder16, stream);
-  if (vt_rc != hipSuccess) return vt_rc;
+  // Work-groups with at most two key blocks each convert them themselves,
+  // unless the caller keeps the images for later chunks.
+  const int longest = (p.q_offset + p.seqlen + kKB8 - 1) / kKB8;
+  const bool direct = !p.keep_images && (split ? p.kb_chunk : longest) <= 2;
+  if (!direct) {
+    const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder16, stream);
+    if (vt_rc != hipSuccess) return vt_rc;
+  }
   switch (head_dim) {
     case 128:
-      hipLaunchKernelGGL(gqa_prefill8_kernel<128>, grid, dim3(kWaves8 * 64), 0, stream, p);
+      if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<128, true>), grid, dim3(kWaves8 * 64), 0, stream, p);
+      else hipLaunchKernelGGL((gqa_prefill8_kernel<128, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
       if (split) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
       break;
     case 256:
-      hipLaunchKernelGGL(gqa_prefill8_kernel<256>, grid, dim3(kWaves8 * 64), 0, stream, p);
+      if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<256, true>), grid, dim3(kWaves8 * 64), 0, stream, p);
+      else hipLaunchKernelGGL((gqa_prefill8_kernel<256, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
       if (split) hipLaunchKernelGGL(prefill_combine_kernel<256>, cgrid, dim3(256), 0, stream, p);
       break;
     default: return hipErrorInvalidValue;

@@ -296,3 +296,44 @@ def test_chunked_prefill_with_kept_images_equals_fresh_images(hip_backend, heads
     got = hip_backend.attention_prefill(q_all[500:600], k2[:600], v2[:600], scale, q_offset=500, images=images)
     want = hip_backend.attention_prefill(q_all[500:600], k2[:600], v2[:600], scale, q_offset=500)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("steps,q_offset,heads,kv,dim", [
+    (1, 0, 8, 2, 256), (64, 0, 8, 2, 256), (100, 0, 8, 2, 256), (128, 0, 8, 2, 256), (128, 0, 16, 2, 256),
+    (300, 0, 8, 2, 256), (512, 0, 8, 2, 256), (512, 0, 4, 4, 128), (128, 0, 2, 2, 128), (40, 17, 8, 2, 256),
+    (100, 28, 8, 1, 256),
+])
+@pytest.mark.parametrize("pattern", ["normal", "large_v_tiny_k", "blockwise"])
+def test_short_prompt_direct_tiles_equal_images(hip_backend, steps, q_offset, heads, kv, dim, pattern):
+    """Short prompts (at most two 64-key blocks per work-group) convert K and V
+    inside the main kernel instead of through the image pre-pass: the result
+    equals, bit for bit, the image path (the kept-image entry point always
+    takes it), and both match the oracle."""
+    total = q_offset + steps
+    g = torch.Generator().manual_seed(steps * 7 + heads + dim + q_offset)
+    q = torch.randn(steps, heads, dim, generator=g)
+    k = torch.randn(total, kv, dim, generator=g)
+    v = torch.randn(total, kv, dim, generator=g)
+    if pattern != "normal":
+        # bf16-valued q converts to fp16 exactly; with f32 q, its fp16 rounding
+        # error grows with the score scale (K up to 4x unit magnitude here) and
+        # would reach the gate by itself (unit-magnitude K: the normal pattern)
+        q = q.to(torch.bfloat16).float()
+    if pattern == "large_v_tiny_k":
+        v, k = v * 3e4, k * 1e-3
+    elif pattern == "blockwise":  # a different magnitude in every 64-key block
+        for b in range(0, total, 64):
+            v[b : b + 64] *= 10.0 ** (b // 64 % 5 - 2)
+            k[b : b + 64] *= 2.0 ** (b // 64 % 3)
+    k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    scale = dim**-0.5
+    print(f"[direct] S={steps} off={q_offset} H={heads} Hkv={kv} D={dim} {pattern}", flush=True)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    direct = hip_backend.attention_prefill(qd, kd, vd, scale, q_offset=q_offset)
+    images = hip_backend.prefill_images(total, kv, dim)
+    via_images = hip_backend.attention_prefill(qd, kd, vd, scale, q_offset=q_offset, images=images)
+    assert torch.equal(direct, via_images)
+    ref = orc.torch_prefill_banded(q, k.float(), v.float(), q_offset, scale)
+    amax = orc.torch_prefill_banded(q, k.float(), v.float().abs(), q_offset, scale).abs()
+    err = (direct.cpu() - ref).abs()
+    assert bool((err <= 2e-3 * torch.clamp(amax, min=1.0)).all()), float(err.max())
