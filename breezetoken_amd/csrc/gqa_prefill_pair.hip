@@ -17,8 +17,9 @@
 //    N-1-j of one kv head: together they need N+1 steps whatever j is, so
 //    every work-group does the same work.  A runs block j, then the first
 //    keys of block N-1-j; B runs the remaining keys of block N-1-j; both take
-//    ceil((N+1)/2) steps in lockstep (one barrier per step), and the two
-//    halves of block N-1-j are merged through LDS at the end;
+//    ceil((N+1)/2) steps in lockstep (two barrier phases per step: one group
+//    runs Q.K^T + softmax while the other runs P.V), and the two halves of
+//    block N-1-j are merged through LDS at the end;
 //  * Q.K^T runs on fp16 MFMAs: q (f32, as the reference keeps it through
 //    prefill.py:49-68, or bf16) is rounded to fp16 after scaling each query
 //    row by a power of two, and K comes from the pre-pass's fp16 image, scaled
