@@ -85,7 +85,13 @@ struct PrefillParams {
   // its log2-domain LSE per (query, head) row and chunk, merged by
   // prefill_combine_kernel.  kb_chunk = 0: one work-group per query block.
   int32_t kb_chunk;
-  int32_t max_chunks;  // chunks of the longest query block (grid z)
+  // Paired split (pair_parts > 0, kb_chunk = 0): query blocks nqb-1-r and r
+  // form pair r; the pair's key blocks (those of nqb-1-r, then those of r) are
+  // cut into pair_parts equal ranges, one per work-group (grid x = pairs x
+  // pair_parts), each covering at most two segments; a query block covered
+  // by more than one range writes partials for prefill_combine_kernel.
+  int32_t pair_parts;
+  int32_t max_chunks;  // chunks of the longest query block (grid z of the uniform split)
   float* part;         // (kv_heads, query blocks, max_chunks, 128 rows, D) f32
   float* lse;          // (kv_heads, query blocks, max_chunks, 128 rows) f32
 };
@@ -93,11 +99,14 @@ struct PrefillParams {
 // Split-key plan of the two-waves-per-SIMD prefill: used when one work-group
 // per query block would leave CUs idle (short prompts, long cached prefixes).
 struct PrefillSplitPlan {
-  int32_t kb_chunk = 0;    // 0: no split
+  int32_t kb_chunk = 0;    // 0: no uniform split
+  int32_t pair_parts = 0;  // 0: no paired split
   int32_t max_chunks = 1;
   int32_t query_blocks = 0;
   size_t part_rows = 0;    // kv_heads x query_blocks x max_chunks x rows per work-group
   size_t part_bytes = 0;   // part_rows x (head_dim f32 partials + 1 f32 LSE)
+  bool active() const { return kb_chunk > 0 || pair_parts > 0; }
+  bool uses_partials() const { return kb_chunk > 0 || (pair_parts > 0 && max_chunks > 1); }
 };
 PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv_heads, int head_dim,
                                      int num_cus);

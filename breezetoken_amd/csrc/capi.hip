@@ -447,7 +447,7 @@ int64_t bt_prefill_split_workspace_bytes(int32_t seqlen, int32_t q_offset, int32
   const int64_t vt = prefill_base_bytes(q_offset + seqlen, kv_heads, head_dim);
   int64_t part_offset = 0;
   const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
-  return plan.kb_chunk > 0 ? part_offset + (int64_t)plan.part_bytes : vt;
+  return plan.uses_partials() ? part_offset + (int64_t)plan.part_bytes : vt;
 }
 
 // Shared by bt_gqa_prefill and bt_gqa_prefill_cached: validates the call and
@@ -517,15 +517,19 @@ static int prefill_run(const void* q, int32_t q_dtype, const void* k, const void
   // Group sizes 1, 2, 4, 8 at D = 128 / 256 run two waves per SIMD; other
   // shapes take the one-wave-per-SIMD kernel (each reads the image order its
   // MFMA shape needs).  When one work-group per query block would leave CUs
-  // idle and `partials` holds the plan's partials, the key range is split.
+  // idle or the causal triangle's work is uneven, and `partials` holds the
+  // plan's partials (if it needs any), the key ranges are split.
   if (bt::prefill8_serves(p.group, head_dim)) {
     int64_t part_offset = 0;
     const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
-    if (plan.kb_chunk > 0 && partials && partials_bytes >= (int64_t)plan.part_bytes) {
+    if (plan.active() && (!plan.uses_partials() || (partials && partials_bytes >= (int64_t)plan.part_bytes))) {
       p.kb_chunk = plan.kb_chunk;
+      p.pair_parts = plan.pair_parts;
       p.max_chunks = plan.max_chunks;
-      p.part = static_cast<float*>(partials);
-      p.lse = p.part + plan.part_rows * (size_t)head_dim;
+      if (plan.uses_partials()) {
+        p.part = static_cast<float*>(partials);
+        p.lse = p.part + plan.part_rows * (size_t)head_dim;
+      }
     }
     return hip_rc(bt::launch_prefill8(p, head_dim, (hipStream_t)stream));
   }
@@ -558,7 +562,7 @@ int64_t bt_prefill_partials_bytes(int32_t seqlen, int32_t q_offset, int32_t head
   if ((int64_t)q_offset + seqlen > INT32_MAX) return 0;
   int64_t part_offset = 0;
   const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
-  return plan.kb_chunk > 0 ? (int64_t)plan.part_bytes : 0;
+  return plan.uses_partials() ? (int64_t)plan.part_bytes : 0;
 }
 
 int bt_gqa_prefill_cached(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,

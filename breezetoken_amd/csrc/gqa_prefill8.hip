@@ -74,6 +74,17 @@ __device__ __forceinline__ uint32_t pack_rne8(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2v_8){a, b}, half2v_8));
 }
 
+// Chunks of query block qb under the paired split (see PrefillParams): the
+// ranges of its pair that reach its key blocks.
+template <typename NB>
+__host__ __device__ inline int pair_chunks(int qb, int nqb, int parts, NB n_blocks) {
+  const int r = qb < nqb - 1 - qb ? qb : nqb - 1 - qb;
+  const int qhi = nqb - 1 - r;
+  const int nhi = n_blocks(qhi), nlo = r != qhi ? n_blocks(r) : 0;
+  const int size = (nhi + nlo + parts - 1) / parts;
+  return qb == qhi ? (nhi + size - 1) / size : (nhi + nlo - 1) / size - nhi / size + 1;
+}
+
 }  // namespace
 
 // DIRECT: a work-group with at most two key blocks converts them from the bf16
@@ -113,407 +124,431 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   const int nkeys = P0 + S;
   const int nqb = (S + pos_per_wg - 1) / pos_per_wg;
   const int nblk = (nkeys + kKB8 - 1) / kKB8;
-  const int qblk = nqb - 1 - (int)blockIdx.x;  // heavy blocks first
-  const int wg_q0 = qblk * pos_per_wg;
-  const int q0 = wg_q0 + (wave / G) * kQ8;
-  const int wg_qend = min(S, wg_q0 + pos_per_wg);
-  const int nkb = (P0 + wg_qend + kKB8 - 1) / kKB8;
-  // Key blocks [kb0, kb1) of this work-group: all of them, or chunk blockIdx.z.
-  const int chunk = blockIdx.z;
-  int kb0 = 0, kb1 = nkb, nchunks = 1;
-  if (p.kb_chunk > 0) {
-    kb0 = chunk * p.kb_chunk;
-    kb1 = min(nkb, kb0 + p.kb_chunk);
-    nchunks = (nkb + p.kb_chunk - 1) / p.kb_chunk;
-    if (kb0 >= kb1) return;  // this query block has fewer chunks (whole work-group)
-  }
-  const int last = kb1 - 1;
-  const int head = kvh * G + wave % G;
+  // One segment: key blocks [kb0, kb1) of query block qblk, chunk `chunk` of
+  // its nchunks (nchunks > 1: the segment writes a partial for the combine).
+  auto segment = [&](const int qblk, const int kb0, const int kb1, const int chunk, const int nchunks) {
+    const int wg_q0 = qblk * pos_per_wg;
+    const int q0 = wg_q0 + (wave / G) * kQ8;
+    const int last = kb1 - 1;
+    const int head = kvh * G + wave % G;
 
-  const size_t head_img = (size_t)kvh * p.img_blocks * kKB8 * D;  // this kv head's images
-  const __amdgpu_buffer_rsrc_t krs = rsrc8(p.kimg + head_img, (uint32_t)nblk * kImg);
-  const __amdgpu_buffer_rsrc_t vrs = rsrc8(p.vt + head_img, (uint32_t)nblk * kImg);
-  const int* kexp = p.kexp + kvh * p.img_blocks;
-  const uint32_t v_voff = (uint32_t)lane * 16;
-  // Tile copy i (1 KiB) is bytes [1024 i, +1024) of the block's K or V^T
-  // image; the K image is row-major with 16-byte slot s of row r holding chunk
-  // s ^ (r & 15), so the tile lands swizzled.  Wave w issues copies w, w + 8, ...
-  auto copy_k = [&](auto b, int kb) {
-    const uint32_t so = (uint32_t)kb * kImg;
-#pragma unroll
-    for (int j = 0; j < kCopies; ++j) {
-      const int i = wave + kWaves8 * j;
-      dma16_8(krs, k_buf(b) + i * 1024, v_voff, so + (uint32_t)i * 1024);
-    }
-  };
-  auto copy_v = [&](auto b, int kb) {
-    const uint32_t so = (uint32_t)kb * kImg;
-#pragma unroll
-    for (int j = 0; j < kCopies; ++j) {
-      const int i = wave + kWaves8 * j;
-      dma16_8(vrs, v_buf(b) + i * 1024, v_voff, so + (uint32_t)i * 1024);
-    }
-  };
-  // Each wave waits for its own copies; the barrier that follows publishes
-  // them.  vmcnt counts a wave's loads in issue order, so naming how many
-  // tiles (kCopies loads each) were issued after the awaited one waits for
-  // exactly that tile and the older ones.
-  auto wait_all = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };
-  static_assert(2 * kCopies < 64, "vmcnt holds 6 bits");
-  auto wait_tiles = [](int younger) {
-    if (younger >= 2) __builtin_amdgcn_s_waitcnt(0x0f70 | ((2 * kCopies) & 0xf) | (((2 * kCopies) >> 4) << 14));
-    else if (younger == 1) __builtin_amdgcn_s_waitcnt(0x0f70 | (kCopies & 0xf) | ((kCopies >> 4) << 14));
-    else __builtin_amdgcn_s_waitcnt(0x0f70);
-  };
-  // Work-group barrier without __syncthreads' fence (which would wait for
-  // every copy in flight); the LDS reads before it were consumed by MFMAs.
-  auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    const size_t head_img = (size_t)kvh * p.img_blocks * kKB8 * D;  // this kv head's images
+    const __amdgpu_buffer_rsrc_t krs = rsrc8(p.kimg + head_img, (uint32_t)nblk * kImg);
+    const __amdgpu_buffer_rsrc_t vrs = rsrc8(p.vt + head_img, (uint32_t)nblk * kImg);
+    const int* kexp = p.kexp + kvh * p.img_blocks;
+    const uint32_t v_voff = (uint32_t)lane * 16;
+    // Tile copy i (1 KiB) is bytes [1024 i, +1024) of the block's K or V^T
+    // image; the K image is row-major with 16-byte slot s of row r holding chunk
+    // s ^ (r & 15), so the tile lands swizzled.  Wave w issues copies w, w + 8, ...
+    auto copy_k = [&](auto b, int kb) {
+      const uint32_t so = (uint32_t)kb * kImg;
+  #pragma unroll
+      for (int j = 0; j < kCopies; ++j) {
+        const int i = wave + kWaves8 * j;
+        dma16_8(krs, k_buf(b) + i * 1024, v_voff, so + (uint32_t)i * 1024);
+      }
+    };
+    auto copy_v = [&](auto b, int kb) {
+      const uint32_t so = (uint32_t)kb * kImg;
+  #pragma unroll
+      for (int j = 0; j < kCopies; ++j) {
+        const int i = wave + kWaves8 * j;
+        dma16_8(vrs, v_buf(b) + i * 1024, v_voff, so + (uint32_t)i * 1024);
+      }
+    };
+    // Each wave waits for its own copies; the barrier that follows publishes
+    // them.  vmcnt counts a wave's loads in issue order, so naming how many
+    // tiles (kCopies loads each) were issued after the awaited one waits for
+    // exactly that tile and the older ones.
+    auto wait_all = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };
+    static_assert(2 * kCopies < 64, "vmcnt holds 6 bits");
+    auto wait_tiles = [](int younger) {
+      if (younger >= 2) __builtin_amdgcn_s_waitcnt(0x0f70 | ((2 * kCopies) & 0xf) | (((2 * kCopies) >> 4) << 14));
+      else if (younger == 1) __builtin_amdgcn_s_waitcnt(0x0f70 | (kCopies & 0xf) | ((kCopies >> 4) << 14));
+      else __builtin_amdgcn_s_waitcnt(0x0f70);
+    };
+    // Work-group barrier without __syncthreads' fence (which would wait for
+    // every copy in flight); the LDS reads before it were consumed by MFMAs.
+    auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
-  const int i16 = lane & 15;   // query column of the 16x16 tiles
-  const int g4 = lane >> 4;    // lane group: k slice of the operands, rows 4*g4.. of results
+    const int i16 = lane & 15;   // query column of the 16x16 tiles
+    const int g4 = lane >> 4;    // lane group: k slice of the operands, rows 4*g4.. of results
 
-  // Q^T operand: lane holds Q[q0 + i16][st*32 + g4*8 .. +8] for each 32-d step
-  // as fp16, the row scaled by 2^-eq so its largest |q| lies in [2^14, 2^15);
-  // c_col = scale * log2(e) * 2^eq restores it in the exp2 argument.
-  // K and V^T scale exponents of a block, read through the scalar cache a
-  // block ahead of their use (each read is a dependent round trip to memory
-  // the pre-pass just wrote).
-  const int* vexp = p.vexp + kvh * p.img_blocks;
-  int dek[2] = {0, 0}, deb[2] = {kVExpZero, kVExpZero};  // DIRECT: exponents of blocks kb0, kb0 + 1
-  auto scales = [&](int kb, int& ek, int& eb) {
+    // Q^T operand: lane holds Q[q0 + i16][st*32 + g4*8 .. +8] for each 32-d step
+    // as fp16, the row scaled by 2^-eq so its largest |q| lies in [2^14, 2^15);
+    // c_col = scale * log2(e) * 2^eq restores it in the exp2 argument.
+    // K and V^T scale exponents of a block, read through the scalar cache a
+    // block ahead of their use (each read is a dependent round trip to memory
+    // the pre-pass just wrote).
+    const int* vexp = p.vexp + kvh * p.img_blocks;
+    int dek[2] = {0, 0}, deb[2] = {kVExpZero, kVExpZero};  // DIRECT: exponents of blocks kb0, kb0 + 1
+    auto scales = [&](int kb, int& ek, int& eb) {
+      if constexpr (DIRECT) {
+        const bool second = min(kb, last) > kb0;
+        ek = second ? dek[1] : dek[0];
+        eb = second ? deb[1] : deb[0];
+      } else {
+        const int b = min(kb, last);
+        ek = sload(kexp, b);
+        eb = sload(vexp, b);
+      }
+    };
+    // Copy schedule (as in the one-wave kernel):
+    //   start of step kb: V_kb -> V buffer kb % 2; after the mid barrier: K_{kb+2}
+    //   -> K buffer kb % 2; the mid barrier publishes V_{kb-1}, the end barrier
+    //   K_{kb+1}.  No copy goes past the last block (a short work-group would
+    //   otherwise wait for them at its end).
+    // Buffers alternate from the work-group's first block kb0.  The first tiles,
+    // and V_{kb0+1} (which the generic schedule would issue a step later), go out
+    // before the q loads, so their latencies overlap.
+    // DIRECT: threads 0..255 hold V items (chunk c, 8-column slice dc: the 8
+    // keys of chunk c at those columns), threads 256..511 K units (16-byte slot
+    // of a key row), for both blocks; loads go out before the q loads.
+    constexpr int kDC = D / 8;                 // 16-byte column chunks per row
+    constexpr int kVItems = 8 * kDC;           // V^T items per block
+    constexpr int kKPer = kKB8 * kDC / 256;    // K units per K thread per block
+    static_assert(kVItems <= 256 && kKPer >= 1, "head_dim 128 or 256");
+    u32x4 draw[2][8];
     if constexpr (DIRECT) {
-      const bool second = min(kb, last) > kb0;
-      ek = second ? dek[1] : dek[0];
-      eb = second ? deb[1] : deb[0];
+      const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
+      const uint32_t range = (uint32_t)nkeys * row_bytes;  // keys past the prompt read as zero
+      if (t < 256) {
+        const __amdgpu_buffer_rsrc_t vsrc = rsrc8(p.v + (int64_t)kvh * p.kv_stride_head, range);
+        const int c = t / kDC, dc = t % kDC;
+  #pragma unroll
+        for (int b = 0; b < 2; ++b)
+          if (t < kVItems && kb0 + b <= last)
+  #pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int key = (kb0 + b) * kKB8 + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16;
+              draw[b][j] = load16_8(vsrc, (uint32_t)key * row_bytes + (uint32_t)dc * 16);
+            }
+      } else {
+        const __amdgpu_buffer_rsrc_t ksrc = rsrc8(p.k + (int64_t)kvh * p.kv_stride_head, range);
+  #pragma unroll
+        for (int b = 0; b < 2; ++b)
+          if (kb0 + b <= last)
+  #pragma unroll
+            for (int j = 0; j < kKPer; ++j) {
+              const int x = j * 256 + (t - 256);
+              const int r = x / kDC, slot = x % kDC;
+              draw[b][j] = load16_8(ksrc, (uint32_t)((kb0 + b) * kKB8 + r) * row_bytes + (uint32_t)(slot ^ (r & 15)) * 16);
+            }
+      }
     } else {
-      const int b = min(kb, last);
-      ek = sload(kexp, b);
-      eb = sload(vexp, b);
+      copy_k(Buf8<0>{}, kb0);
+      if (kb0 + 1 <= last) copy_k(Buf8<1>{}, kb0 + 1);
+      copy_v(Buf8<0>{}, kb0);
+      if (kb0 + 1 <= last) copy_v(Buf8<1>{}, kb0 + 1);
     }
-  };
-  // Copy schedule (as in the one-wave kernel):
-  //   start of step kb: V_kb -> V buffer kb % 2; after the mid barrier: K_{kb+2}
-  //   -> K buffer kb % 2; the mid barrier publishes V_{kb-1}, the end barrier
-  //   K_{kb+1}.  No copy goes past the last block (a short work-group would
-  //   otherwise wait for them at its end).
-  // Buffers alternate from the work-group's first block kb0.  The first tiles,
-  // and V_{kb0+1} (which the generic schedule would issue a step later), go out
-  // before the q loads, so their latencies overlap.
-  // DIRECT: threads 0..255 hold V items (chunk c, 8-column slice dc: the 8
-  // keys of chunk c at those columns), threads 256..511 K units (16-byte slot
-  // of a key row), for both blocks; loads go out before the q loads.
-  constexpr int kDC = D / 8;                 // 16-byte column chunks per row
-  constexpr int kVItems = 8 * kDC;           // V^T items per block
-  constexpr int kKPer = kKB8 * kDC / 256;    // K units per K thread per block
-  static_assert(kVItems <= 256 && kKPer >= 1, "head_dim 128 or 256");
-  u32x4 draw[2][8];
-  if constexpr (DIRECT) {
-    const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
-    const uint32_t range = (uint32_t)nkeys * row_bytes;  // keys past the prompt read as zero
-    if (t < 256) {
-      const __amdgpu_buffer_rsrc_t vsrc = rsrc8(p.v + (int64_t)kvh * p.kv_stride_head, range);
-      const int c = t / kDC, dc = t % kDC;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-        if (t < kVItems && kb0 + b <= last)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int key = (kb0 + b) * kKB8 + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16;
-            draw[b][j] = load16_8(vsrc, (uint32_t)key * row_bytes + (uint32_t)dc * 16);
-          }
-    } else {
-      const __amdgpu_buffer_rsrc_t ksrc = rsrc8(p.k + (int64_t)kvh * p.kv_stride_head, range);
-#pragma unroll
+    int ek_c, eb_c;
+    if constexpr (!DIRECT) scales(kb0, ek_c, eb_c);
+    u32x4 qop[kDSteps];
+    float c_col;
+    {
+      const int qrow = min(q0 + i16, S - 1);
+      const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + g4 * 8;
+      const int eq = q_row_f16(p.q, p.q_f32 != 0, off, 32, qop, [](uint32_t mx) {
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
+        return max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+      });
+      c_col = __builtin_ldexpf(p.scale_log2, eq);
+    }
+    if constexpr (DIRECT) {
+      // Block maxima (bf16 bits of |x|, which order like |x|): V over waves
+      // 0..3, K over waves 4..7; then every thread derives the same exponents.
+      uint32_t mx[2] = {0u, 0u};
+      const int nj = t < 256 ? (t < kVItems ? 8 : 0) : kKPer;
+  #pragma unroll
       for (int b = 0; b < 2; ++b)
         if (kb0 + b <= last)
-#pragma unroll
-          for (int j = 0; j < kKPer; ++j) {
-            const int x = j * 256 + (t - 256);
-            const int r = x / kDC, slot = x % kDC;
-            draw[b][j] = load16_8(ksrc, (uint32_t)((kb0 + b) * kKB8 + r) * row_bytes + (uint32_t)(slot ^ (r & 15)) * 16);
+  #pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (j < nj)
+  #pragma unroll
+              for (int i = 0; i < 4; ++i)
+                mx[b] = max(mx[b], max(draw[b][j][i] & 0x7fffu, (draw[b][j][i] >> 16) & 0x7fffu));
+  #pragma unroll
+      for (int b = 0; b < 2; ++b) {
+  #pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx[b] = max(mx[b], (uint32_t)__shfl_xor((int)mx[b], o, 64));
+        if (lane == 0) dmax[b][wave] = mx[b];
+      }
+      __syncthreads();
+  #pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const uint32_t vm = max(max(dmax[b][0], dmax[b][1]), max(dmax[b][2], dmax[b][3]));
+        const uint32_t km = max(max(dmax[b][4], dmax[b][5]), max(dmax[b][6], dmax[b][7]));
+        if (km != 0) {
+          const int ebits = (int)(km >> 7);
+          dek[b] = (ebits == 0 ? 1 : ebits) - 127 - 14;
+        }
+        if (vm != 0) {
+          const int ebits = (int)(vm >> 7);
+          const int E = (ebits == 0 ? 1 : ebits) - 127;
+          deb[b] = E <= 14 ? -4 * ((14 - E) / 4) : 4 * ((E - 14 + 3) / 4);  // 4 * ceil((E - 14) / 4)
+        }
+      }
+      auto to_f16 = [](float a, float b, int e) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                                (float2v_8){__builtin_ldexpf(a, -e), __builtin_ldexpf(b, -e)}, half2v_8));
+      };
+      auto write_tiles = [&](auto bsel) {
+        constexpr int b = decltype(bsel)::value;
+        if (kb0 + b > last) return;
+        if (t < 256) {
+          if (t >= kVItems) return;
+          const int c = t / kDC, dc = t % kDC;
+          const int e = deb[b];
+  #pragma unroll
+          for (int i = 0; i < 8; ++i) {  // V^T row d = dc*8 + i of chunk c
+            u32x4 o;
+  #pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const uint32_t w0 = draw[b][2 * m][i >> 1], w1 = draw[b][2 * m + 1][i >> 1];
+              o[m] = to_f16(__uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16)),
+                            __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16)), e);
+            }
+            *reinterpret_cast<u32x4*>(v_buf(bsel) + (c * D + dc * 8 + i) * 16) = o;
           }
+        } else {
+          const int e = dek[b];
+  #pragma unroll
+          for (int j = 0; j < kKPer; ++j) {  // unit x lands at x * 16: row x / kDC, slot x % kDC
+            u32x4 o;
+  #pragma unroll
+            for (int m = 0; m < 4; ++m)
+              o[m] = to_f16(__uint_as_float(draw[b][j][m] << 16), __uint_as_float(draw[b][j][m] & 0xffff0000u), e);
+            *reinterpret_cast<u32x4*>(k_buf(bsel) + (j * 256 + (t - 256)) * 16) = o;
+          }
+        }
+      };
+      write_tiles(Buf8<0>{});
+      write_tiles(Buf8<1>{});
+      scales(kb0, ek_c, eb_c);
+    }
+
+    floatx4 oacc[kDTiles];
+  #pragma unroll
+    for (int i = 0; i < kDTiles; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_ref = -INFINITY;          // reference max (log2 domain) of this lane's query column
+    float l_run = 0.f;                // partial row sum over this lane's keys
+    int e_run = kVExpZero;            // V scale O is kept in: O_true = O * 2^e_run
+    const int my_q = q0 + i16;
+    const int my_pos = P0 + my_q;     // keys 0 .. my_pos
+    u32x4 pk[2];                      // P of the pending block: 32-key halves, fp16
+
+    // S^T (64 keys x 16 queries) = K . Q^T from K buffer b: A operand of d-step
+    // st / key sub-tile sub is chunk st*4 + g4 of key row sub*16 + i16, stored
+    // in slot (st*4 + g4) ^ i16 of that row (row & 15 == i16).
+    auto qk = [&](auto b, floatx4 (&sacc)[4]) {
+      const unsigned char* kb_ = k_buf(b);
+      const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+      for (int st = 0; st < kDSteps; ++st) {
+  #pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(kb_ + (sub * 16 + i16) * (D * 2) +
+                                                            (((st * 4 + g4) ^ i16) * 16));
+          sacc[sub] = mfma16_f16(a, qop[st], st == 0 ? zero : sacc[sub]);
+        }
+      }
+    };
+    // O^T += V^T . P^T over the 64 keys of V^T buffer b: A operand of key half kh
+    // / d tile dt is chunk kh*4 + g4 of row dt*16 + i16.
+    auto pv = [&](auto b, const u32x4 (&pp)[2]) {
+      const unsigned char* vb_ = v_buf(b);
+  #pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+  #pragma unroll
+        for (int dt = 0; dt < kDTiles; ++dt) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(vb_ + ((kh * 4 + g4) * D + dt * 16 + i16) * 16);
+          oacc[dt] = mfma16_f16(a, pp[kh], oacc[dt]);
+        }
+      }
+    };
+    // Causal mask of block kb: score of key sub*16 + g4*4 + r for query my_q.
+    auto mask = [&](int kb, floatx4 (&sacc)[4]) {
+      const int key0 = kb * kKB8 + g4 * 4;
+  #pragma unroll
+      for (int sub = 0; sub < 4; ++sub)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = key0 + sub * 16 + r;
+          sacc[sub][r] = key <= my_pos ? sacc[sub][r] : -INFINITY;
+        }
+    };
+    // Online softmax of block kb: max over the 64 keys of the column (this
+    // lane's 16 and three lane groups' via xor 16 / 32), lazy reference update,
+    // P as fp16 in the MFMA key order; returns the factor O must be scaled by.
+    // The V^T block's power-of-two scale enters P' = P * 2^shift through the
+    // exp2 bias; the row sum takes P.
+    auto softmax = [&](floatx4 (&sacc)[4], u32x4 (&out)[2], int ek, int eb) -> float {
+      float tmax = -INFINITY;
+  #pragma unroll
+      for (int sub = 0; sub < 4; ++sub)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[sub][r]);
+      const float c_log2 = __builtin_ldexpf(c_col, ek);  // with the K block's scale
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = halves_max(tmax) * c_log2;
+      const bool move = tmax > m_ref + kLazy8;
+      const float m_new = move ? tmax : m_ref;
+      const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
+      m_ref = m_new;
+      const int e_new = vexp_next(e_run, eb);
+      const int shift = vexp_shift(e_new, eb);
+      const float neg_m = (m_ref == -INFINITY ? 0.f : -m_ref) + (float)shift;
+      float psum = 0.f;
+  #pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const floatx4& s = sacc[2 * kh + (j >> 1)];
+          const float e0 = fast_exp2(fmaf(s[(j & 1) * 2], c_log2, neg_m));
+          const float e1 = fast_exp2(fmaf(s[(j & 1) * 2 + 1], c_log2, neg_m));
+          psum += e0 + e1;
+          out[kh][j] = pack_rne8(e0, e1);
+        }
+      }
+      if (shift != 0) psum = __builtin_ldexpf(psum, -shift);  // wave-uniform, rare
+      l_run = l_run * alpha + psum;
+      const float factor = e_new != e_run ? __builtin_ldexpf(alpha, e_run - e_new) : alpha;
+      e_run = e_new;
+      return factor;
+    };
+    auto rescale = [&](float alpha) {
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max moved by > 2^8
+  #pragma unroll
+        for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
+      }
+    };
+    const int kb_diag = (P0 + q0 + 1) / kKB8;  // earlier blocks need no mask
+
+    wait_all();
+    __syncthreads();
+    {
+      floatx4 sacc[4];
+      qk(Buf8<0>{}, sacc);
+      barrier();
+      if (kb0 + 2 <= last) copy_k(Buf8<0>{}, kb0 + 2);
+      if (kb0 >= kb_diag) mask(kb0, sacc);
+      int ek_n, eb_n;
+      scales(kb0 + 1, ek_n, eb_n);
+      softmax(sacc, pk, ek_c, eb_c);  // O is still zero: its factor does not matter
+      ek_c = ek_n;
+      eb_c = eb_n;
+      barrier();
+    }
+    // Block kb: A: S_kb = K_kb . Q^T; B: O += V_{kb-1} . P_{kb-1} beside the
+    // softmax of S_kb.
+    auto step = [&](auto b, int kb) {
+      constexpr int B = decltype(b)::value;
+      const bool second = kb == kb0 + 1;  // its V^T went out in the prologue
+      if (!second) copy_v(b, kb);
+      int ek_n, eb_n;
+      scales(kb + 1, ek_n, eb_n);
+      floatx4 sacc[4];
+      qk(b, sacc);
+      // V_{kb-1}; issued after it: K_{kb+1} (if any) and V_kb (in the second
+      // block: V_{kb0+1}, from the prologue).
+      wait_tiles((kb + 1 <= last ? 1 : 0) + 1);
+      barrier();
+      if (kb + 2 <= last) copy_k(b, kb + 2);
+      if (kb >= kb_diag) mask(kb, sacc);
+      pv(Buf8<B ^ 1>{}, pk);
+      u32x4 pk_next[2];
+      const float alpha = softmax(sacc, pk_next, ek_c, eb_c);
+      ek_c = ek_n;
+      eb_c = eb_n;
+      rescale(alpha);
+      pk[0] = pk_next[0];
+      pk[1] = pk_next[1];
+      // K_{kb+1} (if any); issued after it: V_kb (except in the second block,
+      // whose V^T went out in the prologue) and K_{kb+2} (if any).
+      wait_tiles((second ? 0 : 1) + (kb + 2 <= last ? 1 : 0));
+      barrier();
+    };
+    // Every pass of the loop ends with a buffer-0 step, so no path reaches the
+    // loop head with a copy into buffer 1 in flight (the compiler would have to
+    // wait for every copy before the first buffer-1 read); an odd last block
+    // runs after the loop.
+    int kb = kb0 + 1;
+    for (; kb + 1 < kb1; kb += 2) {
+      step(Buf8<1>{}, kb);
+      step(Buf8<0>{}, kb + 1);
+    }
+    if (kb < kb1) step(Buf8<1>{}, kb);
+    wait_all();
+    barrier();
+    if ((last - kb0) & 1) pv(Buf8<1>{}, pk); else pv(Buf8<0>{}, pk);
+
+    // ---- epilogue: row sums over the four lane groups, normalise, store -------
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run = halves_sum(l_run);
+    if (nchunks > 1) {
+      // One chunk of a split query block: normalised partial and LSE of row
+      // (wave, query column) for prefill_combine_kernel.
+      const int64_t slot = ((int64_t)kvh * nqb + qblk) * p.max_chunks + chunk;
+      const int row = wave * kQ8 + i16;
+      float* prow = p.part + (slot * kRows8 + row) * D;
+      const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
+  #pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
+        const int d = dt * 16 + g4 * 4;
+        *reinterpret_cast<float4*>(prow + d) =
+            float4{oacc[dt][0] * inv, oacc[dt][1] * inv, oacc[dt][2] * inv, oacc[dt][3] * inv};
+      }
+      if (g4 == 0) p.lse[slot * kRows8 + row] = l_run > 0.f ? fast_log2(l_run) + m_ref : -INFINITY;
+      return;
+    }
+    if (q0 < S && my_q < S) {
+      const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
+      const int64_t orow = (int64_t)my_q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
+  #pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
+        const int d = dt * 16 + g4 * 4;
+        const float o0 = oacc[dt][0] * inv, o1 = oacc[dt][1] * inv, o2 = oacc[dt][2] * inv, o3 = oacc[dt][3] * inv;
+        if (p.out_bf16) {
+          const u32x2 pk2 = {pack2(f32_to_bf16_bits(o0), f32_to_bf16_bits(o1)),
+                             pack2(f32_to_bf16_bits(o2), f32_to_bf16_bits(o3))};
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
+        } else {
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = float4{o0, o1, o2, o3};
+        }
+      }
+    }
+  };
+  auto n_blocks = [&](int qb) { return (P0 + min(S, (qb + 1) * pos_per_wg) + kKB8 - 1) / kKB8; };
+  if (p.pair_parts > 0) {
+    // Paired split: query blocks nqb-1-r and r (r = blockIdx.x / parts) form
+    // a pair with about the same number of key blocks for every r; the pair's
+    // blocks (those of nqb-1-r, then those of r) are cut into `parts` equal
+    // ranges, one per work-group, so each covers at most two segments.
+    const int parts = p.pair_parts;
+    const int r = (int)blockIdx.x / parts, k = (int)blockIdx.x % parts;
+    const int qhi = nqb - 1 - r, qlo = r;
+    const int nhi = n_blocks(qhi), nlo = qlo != qhi ? n_blocks(qlo) : 0;
+    const int size = (nhi + nlo + parts - 1) / parts;
+    const int r0 = k * size, r1 = min(nhi + nlo, r0 + size);
+    if (r0 >= r1) return;
+    if (r0 < nhi) segment(qhi, r0, min(nhi, r1), k, (nhi + size - 1) / size);
+    if (r1 > nhi) {
+      if (r0 < nhi) __syncthreads();  // every wave is done with the first segment's tiles
+      const int kfirst = nhi / size;   // the pair's first part that reaches block qlo
+      segment(qlo, max(0, r0 - nhi), r1 - nhi, k - kfirst, (nhi + nlo - 1) / size - kfirst + 1);
     }
   } else {
-    copy_k(Buf8<0>{}, kb0);
-    if (kb0 + 1 <= last) copy_k(Buf8<1>{}, kb0 + 1);
-    copy_v(Buf8<0>{}, kb0);
-    if (kb0 + 1 <= last) copy_v(Buf8<1>{}, kb0 + 1);
-  }
-  int ek_c, eb_c;
-  if constexpr (!DIRECT) scales(kb0, ek_c, eb_c);
-  u32x4 qop[kDSteps];
-  float c_col;
-  {
-    const int qrow = min(q0 + i16, S - 1);
-    const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + g4 * 8;
-    const int eq = q_row_f16(p.q, p.q_f32 != 0, off, 32, qop, [](uint32_t mx) {
-      mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
-      return max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
-    });
-    c_col = __builtin_ldexpf(p.scale_log2, eq);
-  }
-  if constexpr (DIRECT) {
-    // Block maxima (bf16 bits of |x|, which order like |x|): V over waves
-    // 0..3, K over waves 4..7; then every thread derives the same exponents.
-    uint32_t mx[2] = {0u, 0u};
-    const int nj = t < 256 ? (t < kVItems ? 8 : 0) : kKPer;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-      if (kb0 + b <= last)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (j < nj)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              mx[b] = max(mx[b], max(draw[b][j][i] & 0x7fffu, (draw[b][j][i] >> 16) & 0x7fffu));
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) mx[b] = max(mx[b], (uint32_t)__shfl_xor((int)mx[b], o, 64));
-      if (lane == 0) dmax[b][wave] = mx[b];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const uint32_t vm = max(max(dmax[b][0], dmax[b][1]), max(dmax[b][2], dmax[b][3]));
-      const uint32_t km = max(max(dmax[b][4], dmax[b][5]), max(dmax[b][6], dmax[b][7]));
-      if (km != 0) {
-        const int ebits = (int)(km >> 7);
-        dek[b] = (ebits == 0 ? 1 : ebits) - 127 - 14;
-      }
-      if (vm != 0) {
-        const int ebits = (int)(vm >> 7);
-        const int E = (ebits == 0 ? 1 : ebits) - 127;
-        deb[b] = E <= 14 ? -4 * ((14 - E) / 4) : 4 * ((E - 14 + 3) / 4);  // 4 * ceil((E - 14) / 4)
-      }
-    }
-    auto to_f16 = [](float a, float b, int e) {
-      return __builtin_bit_cast(uint32_t, __builtin_convertvector(
-                                              (float2v_8){__builtin_ldexpf(a, -e), __builtin_ldexpf(b, -e)}, half2v_8));
-    };
-    auto write_tiles = [&](auto bsel) {
-      constexpr int b = decltype(bsel)::value;
-      if (kb0 + b > last) return;
-      if (t < 256) {
-        if (t >= kVItems) return;
-        const int c = t / kDC, dc = t % kDC;
-        const int e = deb[b];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {  // V^T row d = dc*8 + i of chunk c
-          u32x4 o;
-#pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            const uint32_t w0 = draw[b][2 * m][i >> 1], w1 = draw[b][2 * m + 1][i >> 1];
-            o[m] = to_f16(__uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16)),
-                          __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16)), e);
-          }
-          *reinterpret_cast<u32x4*>(v_buf(bsel) + (c * D + dc * 8 + i) * 16) = o;
-        }
-      } else {
-        const int e = dek[b];
-#pragma unroll
-        for (int j = 0; j < kKPer; ++j) {  // unit x lands at x * 16: row x / kDC, slot x % kDC
-          u32x4 o;
-#pragma unroll
-          for (int m = 0; m < 4; ++m)
-            o[m] = to_f16(__uint_as_float(draw[b][j][m] << 16), __uint_as_float(draw[b][j][m] & 0xffff0000u), e);
-          *reinterpret_cast<u32x4*>(k_buf(bsel) + (j * 256 + (t - 256)) * 16) = o;
-        }
-      }
-    };
-    write_tiles(Buf8<0>{});
-    write_tiles(Buf8<1>{});
-    scales(kb0, ek_c, eb_c);
-  }
-
-  floatx4 oacc[kDTiles];
-#pragma unroll
-  for (int i = 0; i < kDTiles; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_ref = -INFINITY;          // reference max (log2 domain) of this lane's query column
-  float l_run = 0.f;                // partial row sum over this lane's keys
-  int e_run = kVExpZero;            // V scale O is kept in: O_true = O * 2^e_run
-  const int my_q = q0 + i16;
-  const int my_pos = P0 + my_q;     // keys 0 .. my_pos
-  u32x4 pk[2];                      // P of the pending block: 32-key halves, fp16
-
-  // S^T (64 keys x 16 queries) = K . Q^T from K buffer b: A operand of d-step
-  // st / key sub-tile sub is chunk st*4 + g4 of key row sub*16 + i16, stored
-  // in slot (st*4 + g4) ^ i16 of that row (row & 15 == i16).
-  auto qk = [&](auto b, floatx4 (&sacc)[4]) {
-    const unsigned char* kb_ = k_buf(b);
-    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < kDSteps; ++st) {
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(kb_ + (sub * 16 + i16) * (D * 2) +
-                                                          (((st * 4 + g4) ^ i16) * 16));
-        sacc[sub] = mfma16_f16(a, qop[st], st == 0 ? zero : sacc[sub]);
-      }
-    }
-  };
-  // O^T += V^T . P^T over the 64 keys of V^T buffer b: A operand of key half kh
-  // / d tile dt is chunk kh*4 + g4 of row dt*16 + i16.
-  auto pv = [&](auto b, const u32x4 (&pp)[2]) {
-    const unsigned char* vb_ = v_buf(b);
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-#pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(vb_ + ((kh * 4 + g4) * D + dt * 16 + i16) * 16);
-        oacc[dt] = mfma16_f16(a, pp[kh], oacc[dt]);
-      }
-    }
-  };
-  // Causal mask of block kb: score of key sub*16 + g4*4 + r for query my_q.
-  auto mask = [&](int kb, floatx4 (&sacc)[4]) {
-    const int key0 = kb * kKB8 + g4 * 4;
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = key0 + sub * 16 + r;
-        sacc[sub][r] = key <= my_pos ? sacc[sub][r] : -INFINITY;
-      }
-  };
-  // Online softmax of block kb: max over the 64 keys of the column (this
-  // lane's 16 and three lane groups' via xor 16 / 32), lazy reference update,
-  // P as fp16 in the MFMA key order; returns the factor O must be scaled by.
-  // The V^T block's power-of-two scale enters P' = P * 2^shift through the
-  // exp2 bias; the row sum takes P.
-  auto softmax = [&](floatx4 (&sacc)[4], u32x4 (&out)[2], int ek, int eb) -> float {
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[sub][r]);
-    const float c_log2 = __builtin_ldexpf(c_col, ek);  // with the K block's scale
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = halves_max(tmax) * c_log2;
-    const bool move = tmax > m_ref + kLazy8;
-    const float m_new = move ? tmax : m_ref;
-    const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
-    m_ref = m_new;
-    const int e_new = vexp_next(e_run, eb);
-    const int shift = vexp_shift(e_new, eb);
-    const float neg_m = (m_ref == -INFINITY ? 0.f : -m_ref) + (float)shift;
-    float psum = 0.f;
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const floatx4& s = sacc[2 * kh + (j >> 1)];
-        const float e0 = fast_exp2(fmaf(s[(j & 1) * 2], c_log2, neg_m));
-        const float e1 = fast_exp2(fmaf(s[(j & 1) * 2 + 1], c_log2, neg_m));
-        psum += e0 + e1;
-        out[kh][j] = pack_rne8(e0, e1);
-      }
-    }
-    if (shift != 0) psum = __builtin_ldexpf(psum, -shift);  // wave-uniform, rare
-    l_run = l_run * alpha + psum;
-    const float factor = e_new != e_run ? __builtin_ldexpf(alpha, e_run - e_new) : alpha;
-    e_run = e_new;
-    return factor;
-  };
-  auto rescale = [&](float alpha) {
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rare: the max moved by > 2^8
-#pragma unroll
-      for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
-    }
-  };
-  const int kb_diag = (P0 + q0 + 1) / kKB8;  // earlier blocks need no mask
-
-  wait_all();
-  __syncthreads();
-  {
-    floatx4 sacc[4];
-    qk(Buf8<0>{}, sacc);
-    barrier();
-    if (kb0 + 2 <= last) copy_k(Buf8<0>{}, kb0 + 2);
-    if (kb0 >= kb_diag) mask(kb0, sacc);
-    int ek_n, eb_n;
-    scales(kb0 + 1, ek_n, eb_n);
-    softmax(sacc, pk, ek_c, eb_c);  // O is still zero: its factor does not matter
-    ek_c = ek_n;
-    eb_c = eb_n;
-    barrier();
-  }
-  // Block kb: A: S_kb = K_kb . Q^T; B: O += V_{kb-1} . P_{kb-1} beside the
-  // softmax of S_kb.
-  auto step = [&](auto b, int kb) {
-    constexpr int B = decltype(b)::value;
-    const bool second = kb == kb0 + 1;  // its V^T went out in the prologue
-    if (!second) copy_v(b, kb);
-    int ek_n, eb_n;
-    scales(kb + 1, ek_n, eb_n);
-    floatx4 sacc[4];
-    qk(b, sacc);
-    // V_{kb-1}; issued after it: K_{kb+1} (if any) and V_kb (in the second
-    // block: V_{kb0+1}, from the prologue).
-    wait_tiles((kb + 1 <= last ? 1 : 0) + 1);
-    barrier();
-    if (kb + 2 <= last) copy_k(b, kb + 2);
-    if (kb >= kb_diag) mask(kb, sacc);
-    pv(Buf8<B ^ 1>{}, pk);
-    u32x4 pk_next[2];
-    const float alpha = softmax(sacc, pk_next, ek_c, eb_c);
-    ek_c = ek_n;
-    eb_c = eb_n;
-    rescale(alpha);
-    pk[0] = pk_next[0];
-    pk[1] = pk_next[1];
-    // K_{kb+1} (if any); issued after it: V_kb (except in the second block,
-    // whose V^T went out in the prologue) and K_{kb+2} (if any).
-    wait_tiles((second ? 0 : 1) + (kb + 2 <= last ? 1 : 0));
-    barrier();
-  };
-  // Every pass of the loop ends with a buffer-0 step, so no path reaches the
-  // loop head with a copy into buffer 1 in flight (the compiler would have to
-  // wait for every copy before the first buffer-1 read); an odd last block
-  // runs after the loop.
-  int kb = kb0 + 1;
-  for (; kb + 1 < kb1; kb += 2) {
-    step(Buf8<1>{}, kb);
-    step(Buf8<0>{}, kb + 1);
-  }
-  if (kb < kb1) step(Buf8<1>{}, kb);
-  wait_all();
-  barrier();
-  if ((last - kb0) & 1) pv(Buf8<1>{}, pk); else pv(Buf8<0>{}, pk);
-
-  // ---- epilogue: row sums over the four lane groups, normalise, store -------
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run = halves_sum(l_run);
-  if (nchunks > 1) {
-    // One chunk of a split query block: normalised partial and LSE of row
-    // (wave, query column) for prefill_combine_kernel.
-    const int64_t slot = ((int64_t)kvh * nqb + qblk) * p.max_chunks + chunk;
-    const int row = wave * kQ8 + i16;
-    float* prow = p.part + (slot * kRows8 + row) * D;
-    const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) {
-      const int d = dt * 16 + g4 * 4;
-      *reinterpret_cast<float4*>(prow + d) =
-          float4{oacc[dt][0] * inv, oacc[dt][1] * inv, oacc[dt][2] * inv, oacc[dt][3] * inv};
-    }
-    if (g4 == 0) p.lse[slot * kRows8 + row] = l_run > 0.f ? fast_log2(l_run) + m_ref : -INFINITY;
-    return;
-  }
-  if (q0 < S && my_q < S) {
-    const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
-    const int64_t orow = (int64_t)my_q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) {
-      const int d = dt * 16 + g4 * 4;
-      const float o0 = oacc[dt][0] * inv, o1 = oacc[dt][1] * inv, o2 = oacc[dt][2] * inv, o3 = oacc[dt][3] * inv;
-      if (p.out_bf16) {
-        const u32x2 pk2 = {pack2(f32_to_bf16_bits(o0), f32_to_bf16_bits(o1)),
-                           pack2(f32_to_bf16_bits(o2), f32_to_bf16_bits(o3))};
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
-      } else {
-        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = float4{o0, o1, o2, o3};
-      }
+    const int qblk = nqb - 1 - (int)blockIdx.x;  // heavy blocks first
+    const int nkb = n_blocks(qblk);
+    // Key blocks of this work-group: all of them, or chunk blockIdx.z.
+    if (p.kb_chunk > 0) {
+      const int chunk = blockIdx.z;
+      const int kb0 = chunk * p.kb_chunk;
+      if (kb0 >= nkb) return;  // this query block has fewer chunks (whole work-group)
+      segment(qblk, kb0, min(nkb, kb0 + p.kb_chunk), chunk, (nkb + p.kb_chunk - 1) / p.kb_chunk);
+    } else {
+      segment(qblk, 0, nkb, 0, 1);
     }
   }
 }
@@ -537,9 +572,9 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
   const int qblk = nqb - 1 - (int)blockIdx.x;
   const int kvh = blockIdx.y;
   const int wg_q0 = qblk * pos_per_wg;
-  const int wg_qend = min(S, wg_q0 + pos_per_wg);
-  const int nkb = (p.q_offset + wg_qend + kKB8 - 1) / kKB8;
-  const int nchunks = (nkb + p.kb_chunk - 1) / p.kb_chunk;
+  auto n_blocks = [&](int qb) { return (p.q_offset + min(S, (qb + 1) * pos_per_wg) + kKB8 - 1) / kKB8; };
+  const int nchunks = p.pair_parts > 0 ? pair_chunks(qblk, nqb, p.pair_parts, n_blocks)
+                                       : (n_blocks(qblk) + p.kb_chunk - 1) / p.kb_chunk;
   if (nchunks <= 1) return;
   const int64_t slot0 = ((int64_t)kvh * nqb + qblk) * p.max_chunks;
   const int t = threadIdx.x;
@@ -603,30 +638,56 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
   const int nqb = (seqlen + pos_per_wg - 1) / pos_per_wg;
   plan.query_blocks = nqb;
   if (nqb < 1 || kv_heads < 1 || num_cus < 1) return plan;
-  // A grid with a work-group per CU or more is already balanced by the
-  // heavy-first launch order.
-  if ((int64_t)nqb * kv_heads >= num_cus) return plan;
+  auto n_blocks = [&](int qb) { return (q_offset + min(seqlen, (qb + 1) * pos_per_wg) + kKB8 - 1) / kKB8; };
   int nkb_max = 0;
-  for (int qb = 0; qb < nqb; ++qb) {
-    const int qend = min(seqlen, (qb + 1) * pos_per_wg);
-    nkb_max = max(nkb_max, (q_offset + qend + kKB8 - 1) / kKB8);
+  for (int qb = 0; qb < nqb; ++qb) nkb_max = max(nkb_max, n_blocks(qb));
+  // The uniform split.  Its grid (query blocks x kv heads x max_chunks) must
+  // fit the CUs in one round, counting the slots of chunks that start past a
+  // query block's keys and exit at once: at config 4, S = 1024, 3-block chunks
+  // (384 slots) took 45.5 us against 34.4 us for 4-block chunks (256 slots)
+  // and 44.2 us unsplit; at S = 2048, 16-block chunks (256 slots) took 54.7 us
+  // against 62.9 us for 11-block chunks (384 slots) and 71.5 us unsplit.
+  // Chunks are at least two key blocks long (one-block chunks: S = 128 24.5 vs
+  // 22.3 us, S = 256 23.5 vs 25.2 us, S = 512 unchanged) and a query block has
+  // at most kMaxChunks.  A grid with a work-group per CU or more is not split
+  // (the heavy-first launch order balances it as far as it can).
+  int uniform = 0;          // its chunk length (0: no uniform split)
+  int longest = nkb_max;    // key blocks of the busiest work-group
+  if ((int64_t)nqb * kv_heads < num_cus) {
+    const int max_chunks = min(num_cus / (nqb * kv_heads), kMaxChunks);
+    const int lo = max(2, (nkb_max + max_chunks - 1) / max_chunks);
+    if (lo < nkb_max) {
+      uniform = lo;
+      longest = lo;
+    }
   }
-  // The grid (query blocks x kv heads x max_chunks) must fit the CUs in one
-  // round, counting the slots of chunks that start past a query block's keys
-  // and exit at once: at config 4, S = 1024, 3-block chunks (384 slots) took
-  // 45.5 us against 34.4 us for 4-block chunks (256 slots) and 44.2 us unsplit;
-  // at S = 2048, 16-block chunks (256 slots) took 54.7 us against 62.9 us for
-  // 11-block chunks (384 slots) and 71.5 us unsplit.  Chunks are at least two
-  // key blocks long (one-block chunks: S = 128 24.5 vs 22.3 us, S = 256 23.5
-  // vs 25.2 us, S = 512 unchanged) and a query block has at most kMaxChunks.
-  const int slots = num_cus / (nqb * kv_heads);
-  const int max_chunks = min(slots, kMaxChunks);
-  int lo = max(2, (nkb_max + max_chunks - 1) / max_chunks);
-  if (lo >= nkb_max) return plan;  // no query block would split
-  plan.kb_chunk = lo;
-  plan.max_chunks = (nkb_max + lo - 1) / lo;
-  plan.part_rows = (size_t)kv_heads * nqb * plan.max_chunks * kRows8;
-  plan.part_bytes = plan.part_rows * ((size_t)head_dim * 4 + 4);
+  // The paired split balances the causal triangle: a pair of query blocks
+  // has about the same key blocks for every pair.  It pays a second q load
+  // and epilogue in work-groups that cover two segments (counted here as two
+  // key blocks), and its ranges are at least two blocks long.
+  const int npairs = (nqb + 1) / 2;
+  const int parts = max(1, min(num_cus / (npairs * kv_heads), kMaxChunks));
+  int pair_longest = 0;
+  for (int r = 0; r < npairs; ++r) {
+    const int qhi = nqb - 1 - r;
+    const int len = n_blocks(qhi) + (r != qhi ? n_blocks(r) : 0);
+    pair_longest = max(pair_longest, (len + parts - 1) / parts);
+  }
+  if (pair_longest >= 2 && pair_longest + 2 < longest) {
+    plan.pair_parts = parts;
+    int mc = 1;
+    for (int qb = 0; qb < nqb; ++qb) mc = max(mc, pair_chunks(qb, nqb, parts, n_blocks));
+    plan.max_chunks = mc;
+  } else if (uniform > 0) {
+    plan.kb_chunk = uniform;
+    plan.max_chunks = (nkb_max + uniform - 1) / uniform;
+  } else {
+    return plan;
+  }
+  if (plan.uses_partials()) {
+    plan.part_rows = (size_t)kv_heads * nqb * plan.max_chunks * kRows8;
+    plan.part_bytes = plan.part_rows * ((size_t)head_dim * 4 + 4);
+  }
   return plan;
 }
 
@@ -637,14 +698,17 @@ bool prefill8_serves(int group, int head_dim) {
 hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t stream) {
   const int pos_per_wg = kQ8 * (kWaves8 / p.group);
   const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
-  const bool split = p.kb_chunk > 0;
+  const bool paired = p.pair_parts > 0;
+  const bool split = p.kb_chunk > 0 || (paired && p.max_chunks > 1);  // partials and the combine
+  if (paired && p.kb_chunk > 0) return hipErrorInvalidValue;
   if (split && (p.max_chunks < 1 || p.max_chunks > kMaxChunks || !p.part || !p.lse)) return hipErrorInvalidValue;
-  const dim3 grid(nqb, p.kv_heads, split ? p.max_chunks : 1);
+  const dim3 grid = paired ? dim3(((nqb + 1) / 2) * p.pair_parts, p.kv_heads, 1)
+                           : dim3(nqb, p.kv_heads, p.kb_chunk > 0 ? p.max_chunks : 1);
   const dim3 cgrid(nqb, p.kv_heads, kRows8 * head_dim / 4 / 256);
   // Work-groups with at most two key blocks each convert them themselves,
   // unless the caller keeps the images for later chunks.
   const int longest = (p.q_offset + p.seqlen + kKB8 - 1) / kKB8;
-  const bool direct = !p.keep_images && (split ? p.kb_chunk : longest) <= 2;
+  const bool direct = !p.keep_images && !paired && (p.kb_chunk > 0 ? p.kb_chunk : longest) <= 2;
   if (!direct) {
     const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder16, stream);
     if (vt_rc != hipSuccess) return vt_rc;

@@ -260,18 +260,21 @@ def test_gemv_refuses_bad_arguments_and_sizes_its_workspace():
         (512, 16384, 16, 4),
         (256, 4096, 8, 14),
         (512, 0, 8, 4),
-        (2048, 0, 8, 2),
         (1024, 0, 8, 4),
-        # a grid of a work-group per CU or more is not split (8192: the pair kernel)
-        (4096, 0, 8, 0),
+        # the paired split (pairs of query blocks r and nqb-1-r, each cut into
+        # 4 / 2 equal ranges): at most 4 / 2 ranges reach a query block
+        (2048, 0, 8, 4),
+        (4096, 0, 8, 2),
+        # S = 8192 runs the pair kernel
         (8192, 0, 8, 0),
     ],
 )
 def test_prefill_split_plan_sizes(steps, q_offset, heads, max_chunks):
     """The split-key plan on a 256-CU device (the count assumed without a GPU):
     the workspace is the V^T and K images and their block scales plus f32 partials and
-    LSEs of kv_heads x query blocks x max_chunks x 128 rows.  S = 8192 runs the
-    pair kernel, which needs no partials."""
+    LSEs of kv_heads x query blocks x max_chunks x 128 rows (max_chunks: the most
+    ranges of the uniform or paired split that reach one query block).  S = 8192
+    runs the pair kernel, which needs no partials."""
     from breezetoken_amd import _lib
 
     lib = _lib.lib()

@@ -221,14 +221,12 @@ def test_backend_split_keys_switch(hip_backend):
     assert (split - one).abs().max().item() <= 1e-3
 
 
-@pytest.mark.parametrize("steps", [4096, 8192])
-def test_long_prompt_needs_no_split(hip_backend, steps):
-    """Config 4 at S = 4096 / 8192 has a work-group per CU or more: no split (and
-    no extra workspace)."""
+def test_long_prompt_needs_no_split(hip_backend):
+    """Config 4 at S = 8192 runs the pair kernel: no split and no extra workspace."""
     from breezetoken_amd import _lib
 
     lib = _lib.lib()
-    assert lib.bt_prefill_split_workspace_bytes(steps, 0, 8, 2, 256) == lib.bt_prefill_workspace_bytes(steps, 2, 256)
+    assert lib.bt_prefill_split_workspace_bytes(8192, 0, 8, 2, 256) == lib.bt_prefill_workspace_bytes(8192, 2, 256)
 
 
 def test_chunked_prefill_head_major_cache(hip_backend):
@@ -337,3 +335,21 @@ def test_short_prompt_direct_tiles_equal_images(hip_backend, steps, q_offset, he
     amax = orc.torch_prefill_banded(q, k.float(), v.float().abs(), q_offset, scale).abs()
     err = (direct.cpu() - ref).abs()
     assert bool((err <= 2e-3 * torch.clamp(amax, min=1.0)).all()), float(err.max())
+
+
+@pytest.mark.parametrize("steps,heads,kv,dim", [
+    (1500, 8, 2, 256), (2048, 8, 2, 256), (3000, 8, 2, 256), (4096, 8, 2, 256), (2048, 16, 2, 128),
+    (2500, 4, 2, 256), (3333, 8, 1, 128),
+])
+def test_paired_split_prefill(hip_backend, steps, heads, kv, dim):
+    """Mid-length prompts take the paired split (query blocks nqb-1-r and r
+    share the work-groups of pair r, ranges cut evenly, partials merged by the
+    combine): every row matches the oracle; sampled rows are checked against
+    decode attention over their prefix."""
+    q, k, v, scale = _inputs(steps, heads, kv, dim, seed=steps + heads)
+    print(f"[paired] S={steps} H={heads} Hkv={kv} D={dim}", flush=True)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu()
+    ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    _close(out, ref)
+    for i in (0, 1, 63, 64, steps // 2, steps - 2, steps - 1):
+        _close(out[i], orc.torch_attention(q[i].float(), k[: i + 1].float(), v[: i + 1].float(), scale))
