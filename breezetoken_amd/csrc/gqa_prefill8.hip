@@ -91,7 +91,9 @@ __host__ __device__ inline int pair_chunks(int qb, int nqb, int parts, NB n_bloc
 // cache straight into its LDS tiles (the layout and rounding of the images
 // of gqa_prefill_vt.hip, same block scales), so a short prompt needs no
 // pre-pass launch.
-template <int D, bool DIRECT>
+// PAIRED: the paired split (two segments per work-group at most); its own
+// instantiation, so the single-segment kernel keeps one copy of the loop.
+template <int D, bool DIRECT, bool PAIRED>
 __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillParams p) {
   constexpr int kDSteps = D / 32;      // K-dimension steps of Q.K^T (32 per MFMA)
   constexpr int kDTiles = D / 16;      // 16-row d tiles of O^T
@@ -520,7 +522,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     }
   };
   auto n_blocks = [&](int qb) { return (P0 + min(S, (qb + 1) * pos_per_wg) + kKB8 - 1) / kKB8; };
-  if (p.pair_parts > 0) {
+  if constexpr (PAIRED) {
     // Paired split: query blocks nqb-1-r and r (r = blockIdx.x / parts) form
     // a pair with about the same number of key blocks for every r; the pair's
     // blocks (those of nqb-1-r, then those of r) are cut into `parts` equal
@@ -663,8 +665,12 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
   }
   // The paired split balances the causal triangle: a pair of query blocks
   // has about the same key blocks for every pair.  It pays a second q load
-  // and epilogue in work-groups that cover two segments (counted here as two
-  // key blocks), and its ranges are at least two blocks long.
+  // and epilogue in work-groups that cover two segments, more partials, and a
+  // fuller machine per block; it replaces the unsplit grid when its longest
+  // range is under two thirds of the busiest query block's (config 4: S = 3000
+  // and 4096 gain 12% and 17%) and at least two blocks long.  Where the
+  // uniform split applies it measured no better (S = 2048: 9 against 16
+  // blocks, 60.0 vs 59.4 us).
   const int npairs = (nqb + 1) / 2;
   const int parts = max(1, min(num_cus / (npairs * kv_heads), kMaxChunks));
   int pair_longest = 0;
@@ -673,7 +679,7 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
     const int len = n_blocks(qhi) + (r != qhi ? n_blocks(r) : 0);
     pair_longest = max(pair_longest, (len + parts - 1) / parts);
   }
-  if (pair_longest >= 2 && pair_longest + 2 < longest) {
+  if (uniform == 0 && pair_longest >= 2 && 3 * pair_longest < 2 * longest) {
     plan.pair_parts = parts;
     int mc = 1;
     for (int qb = 0; qb < nqb; ++qb) mc = max(mc, pair_chunks(qb, nqb, parts, n_blocks));
@@ -715,13 +721,15 @@ hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t str
   }
   switch (head_dim) {
     case 128:
-      if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<128, true>), grid, dim3(kWaves8 * 64), 0, stream, p);
-      else hipLaunchKernelGGL((gqa_prefill8_kernel<128, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
+      if (paired) hipLaunchKernelGGL((gqa_prefill8_kernel<128, false, true>), grid, dim3(kWaves8 * 64), 0, stream, p);
+      else if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<128, true, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
+      else hipLaunchKernelGGL((gqa_prefill8_kernel<128, false, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
       if (split) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
       break;
     case 256:
-      if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<256, true>), grid, dim3(kWaves8 * 64), 0, stream, p);
-      else hipLaunchKernelGGL((gqa_prefill8_kernel<256, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
+      if (paired) hipLaunchKernelGGL((gqa_prefill8_kernel<256, false, true>), grid, dim3(kWaves8 * 64), 0, stream, p);
+      else if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<256, true, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
+      else hipLaunchKernelGGL((gqa_prefill8_kernel<256, false, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
       if (split) hipLaunchKernelGGL(prefill_combine_kernel<256>, cgrid, dim3(256), 0, stream, p);
       break;
     default: return hipErrorInvalidValue;

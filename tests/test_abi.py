@@ -260,11 +260,12 @@ def test_gemv_refuses_bad_arguments_and_sizes_its_workspace():
         (512, 16384, 16, 4),
         (256, 4096, 8, 14),
         (512, 0, 8, 4),
+        (2048, 0, 8, 2),
         (1024, 0, 8, 4),
         # the paired split (pairs of query blocks r and nqb-1-r, each cut into
-        # 4 / 2 equal ranges): at most 4 / 2 ranges reach a query block
-        (2048, 0, 8, 4),
+        # 2 equal ranges): at most 2 ranges reach a query block
         (4096, 0, 8, 2),
+        (3000, 0, 8, 2),
         # S = 8192 runs the pair kernel
         (8192, 0, 8, 0),
     ],

@@ -68,7 +68,7 @@ def test_paired_ranges_cover_every_block_once(steps, q_offset, group, parts):
         assert all((qb, c) in chunks for c in range(counts.pop()))
 
 
-@pytest.mark.parametrize("steps,heads,kv,dim", [(2048, 8, 2, 256), (3000, 8, 2, 256), (4096, 8, 2, 256), (1500, 8, 2, 256)])
+@pytest.mark.parametrize("steps,heads,kv,dim", [(3000, 8, 2, 256), (4096, 8, 2, 256), (6000, 4, 2, 128)])
 def test_library_plan_matches_paired_chunk_counts(steps, heads, kv, dim):
     """The library's plan (256 CUs without a GPU) for these shapes is the paired
     split with parts = 256 / (pairs x kv heads); its partial buffer holds

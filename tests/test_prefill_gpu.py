@@ -344,8 +344,9 @@ def test_short_prompt_direct_tiles_equal_images(hip_backend, steps, q_offset, he
 def test_paired_split_prefill(hip_backend, steps, heads, kv, dim):
     """Mid-length prompts take the paired split (query blocks nqb-1-r and r
     share the work-groups of pair r, ranges cut evenly, partials merged by the
-    combine): every row matches the oracle; sampled rows are checked against
-    decode attention over their prefix."""
+    combine: S = 3000 and 4096 at H = 8, 2048 at H = 16, 3333 at Hkv = 1) or the
+    uniform one (the others): every row matches the oracle; sampled rows are
+    checked against decode attention over their prefix."""
     q, k, v, scale = _inputs(steps, heads, kv, dim, seed=steps + heads)
     print(f"[paired] S={steps} H={heads} Hkv={kv} D={dim}", flush=True)
     out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu()
