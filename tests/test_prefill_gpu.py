@@ -354,3 +354,17 @@ def test_paired_split_prefill(hip_backend, steps, heads, kv, dim):
     _close(out, ref)
     for i in (0, 1, 63, 64, steps // 2, steps - 2, steps - 1):
         _close(out[i], orc.torch_attention(q[i].float(), k[: i + 1].float(), v[: i + 1].float(), scale))
+
+
+@pytest.mark.parametrize("steps,q_offset,heads,kv", [(3000, 500, 8, 2), (2600, 64, 8, 2)])
+def test_paired_split_chunked_prefill(hip_backend, steps, q_offset, heads, kv):
+    """The paired split behind a cached prefix (each pair's ranges then start
+    inside the prefix blocks): matches the banded oracle."""
+    total = q_offset + steps
+    g = torch.Generator().manual_seed(total)
+    q = torch.randn(steps, heads, 256, generator=g)
+    k = torch.randn(total, kv, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(total, kv, 256, generator=g).to(torch.bfloat16)
+    print(f"[paired chunk] S={steps} off={q_offset}", flush=True)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), 1 / 16, q_offset=q_offset)
+    _close(out, orc.torch_prefill_banded(q, k.float(), v.float(), q_offset, 1 / 16))
