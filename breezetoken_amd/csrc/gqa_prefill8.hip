@@ -28,7 +28,15 @@
 //  * the online softmax (log2 domain, lazy rescaling by 2^8) of block kb runs
 //    beside the P.V product of block kb - 1; tiles are double-buffered with
 //    two barriers per block and every copy issued as soon as its buffer is
-//    free, as in the one-wave kernel.
+//    free, as in the one-wave kernel;
+//  * a work-group runs one or two segments (key-block ranges of a query
+//    block): the whole query block, a chunk of it under the uniform split, or
+//    its share of a query-block pair under the paired split (see
+//    PrefillParams); a segment that is not its query block's only chunk writes
+//    a partial and an LSE per row for prefill_combine_kernel;
+//  * work-groups with at most two key blocks can convert them from the bf16
+//    cache into their LDS tiles themselves (DIRECT), with the pre-pass's
+//    layout, rounding and scales, so a short prompt needs no pre-pass.
 #include "bt_common.h"
 #include "bt_kernels.h"
 
