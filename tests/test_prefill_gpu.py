@@ -48,6 +48,14 @@ def test_c4_prefill_f32_output(hip_backend, steps):
     _close(out, ref)
 
 
+def test_c4_prefill_8192_full_output(hip_backend):
+    """S = 8192, every row against the restated causal SDPA in f32 (pair kernel)."""
+    q, k, v, scale = wl.c4_inputs(8192)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu()
+    ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    _close(out, ref)
+
+
 def test_c4_prefill_8192_sampled_rows(hip_backend):
     """S = 8192: every sampled row i must equal decode attention over keys 0..i."""
     q, k, v, scale = wl.c4_inputs(8192)

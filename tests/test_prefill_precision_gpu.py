@@ -45,6 +45,16 @@ def test_c4_prefill_f32_q_matches_reference_arithmetic(hip_backend, steps):
     assert err <= ATOL and cos >= COS
 
 
+def test_c4_prefill_8192_f32_q_full_output(hip_backend):
+    """The benchmark shape with f32 q: every row against the oracle's f32 SDPA."""
+    q, k, v, scale = wl.c4_inputs(8192, q_f32=True)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale).cpu()
+    ref = orc.torch_prefill_attention(q, k.float(), v.float(), scale)
+    err, cos = orc.compare(out.numpy(), ref.numpy())
+    print(f"[c4 f32 q] S=8192: max-abs {err:.3e} cosine {cos:.9f}", flush=True)
+    assert err <= ATOL and cos >= COS
+
+
 def test_c4_prefill_8192_f32_q_sampled_rows(hip_backend):
     """The benchmark shape with f32 q: sampled rows against decode attention
     over keys 0..i in f32."""
