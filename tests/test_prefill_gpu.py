@@ -376,3 +376,41 @@ def test_paired_split_chunked_prefill(hip_backend, steps, q_offset, heads, kv):
     print(f"[paired chunk] S={steps} off={q_offset}", flush=True)
     out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), 1 / 16, q_offset=q_offset)
     _close(out, orc.torch_prefill_banded(q, k.float(), v.float(), q_offset, 1 / 16))
+
+
+# ------------------------------------------- long prompts: the pair kernel
+def _pair_grid(steps, heads, kv):
+    """Work-groups of the pair kernel (query blocks of 128 / min(G, 8) positions,
+    two per work-group); bt_gqa_prefill runs it when this fills the device."""
+    group = heads // kv
+    hg = min(group, 8)
+    nqb = -(-steps // (128 // hg))
+    return (nqb + 1) // 2 * kv * (group // hg)
+
+
+@pytest.mark.parametrize("steps,heads,kv,dim,q_offset,q_f32", [
+    (4096, 16, 2, 256, 0, False),    # G = 8: the 35B-A3B attention shape
+    (4100, 16, 2, 256, 0, True),     # odd block count (one work-group runs the middle block alone), f32 q
+    (4096, 16, 2, 256, 1000, False),  # behind a cached prefix
+    (8192, 8, 2, 128, 0, False),     # G = 4 at D = 128
+    (8192, 8, 4, 256, 0, False),     # G = 2
+    (8192, 8, 8, 128, 0, True),      # G = 1
+    (8200, 8, 2, 256, 0, False),     # config-4 shape, ragged last block
+])
+def test_pair_kernel_shapes(hip_backend, steps, heads, kv, dim, q_offset, q_f32):
+    """Every group size and head dim the pair kernel serves, at prompt lengths
+    where its grid fills the device: every row against the oracle."""
+    assert _pair_grid(steps, heads, kv) >= hip_backend.num_cus
+    g = torch.Generator().manual_seed(steps + 10 * heads + kv + q_offset)
+    q = torch.randn(steps, heads, dim, generator=g)
+    q = q if q_f32 else q.to(torch.bfloat16)
+    k = torch.randn(q_offset + steps, kv, dim, generator=g).to(torch.bfloat16)
+    v = torch.randn(q_offset + steps, kv, dim, generator=g).to(torch.bfloat16)
+    scale = dim**-0.5
+    print(f"[pair] S={steps} H={heads} Hkv={kv} D={dim} off={q_offset} f32q={q_f32}", flush=True)
+    out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, q_offset=q_offset).cpu()
+    if q_offset:
+        ref = orc.torch_prefill_banded(q.float(), k.float(), v.float(), q_offset, scale)
+    else:
+        ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    _close(out, ref)
