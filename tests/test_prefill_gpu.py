@@ -414,3 +414,14 @@ def test_pair_kernel_shapes(hip_backend, steps, heads, kv, dim, q_offset, q_f32)
     else:
         ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
     _close(out, ref)
+
+
+@pytest.mark.parametrize("steps,heads,kv,dim", [(2048, 6, 2, 256), (1500, 10, 2, 128), (4096, 14, 2, 128),
+                                                (3001, 12, 2, 256)])
+def test_one_wave_kernel_long_prompts(hip_backend, steps, heads, kv, dim):
+    """Group sizes 3, 5, 6, 7 (the one-wave-per-SIMD kernel) on long prompts:
+    every row against the oracle."""
+    q, k, v, scale = _inputs(steps, heads, kv, dim, seed=steps + heads)
+    print(f"[one-wave] S={steps} H={heads} Hkv={kv} D={dim}", flush=True)
+    ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
+    _close(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale), ref)
