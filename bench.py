@@ -480,15 +480,21 @@ def main() -> int:
         del rkv
         torch.cuda.empty_cache()
         # prefill (config 4: bf16 q/k/v, bf16 output), and at S = 8192 also with the
-        # same q draws in f32, as the reference's prefill computes it (prefill.py:49-68)
+        # same q draws in f32, as the reference's prefill computes it (prefill.py:49-68).
+        # Like the decode rows, one graph holds LAYERS calls on LAYERS separate copies of
+        # the inputs (a model's layers), so a short prompt's figure is not the host's
+        # graph-launch rate.
         pre = []
         for s, qf32 in ((128, False), (512, False), (2048, False), (8192, False), (8192, True)):
-            qp, kp, vp, sc = (t.to(dev) if hasattr(t, "to") else t for t in wl.c4_inputs(s, q_f32=qf32))
+            base = [t.to(dev) if hasattr(t, "to") else t for t in wl.c4_inputs(s, q_f32=qf32)]
+            sets = [(base[0].clone(), base[1].clone(), base[2].clone(), base[3]) for _ in range(LAYERS)]
+            del base
             try:
                 # MFMA-heavy work runs ~10% slower for its first ~10 ms in a process (clock
                 # ramp; measured 334 -> 287 us at S = 8192), so the long rows warm up ~30 ms
-                pms = time_graph(torch, lambda: backend.attention_prefill(qp, kp, vp, sc, torch.bfloat16),
-                                 max(20, esteps // 10), 100 if s >= 8192 else 5)
+                pms = time_graph(torch, lambda: [backend.attention_prefill(qp, kp, vp, sc, torch.bfloat16)
+                                                 for qp, kp, vp, sc in sets],
+                                 max(20, esteps // 10), 20 if s >= 8192 else 5) / LAYERS
             except RuntimeError as exc:
                 pre.append({"steps": s, "error": str(exc)[:120]})
                 break
@@ -510,21 +516,26 @@ def main() -> int:
         # the split-key schedule against one work-group per query block, same process
         chunked = []
         for heads, steps, pos0 in CHUNKED_CASES:
-            qc, kc, vc = chunked_inputs(torch, dev, heads, steps, pos0)
+            base = chunked_inputs(torch, dev, heads, steps, pos0)
+            sets = [tuple(t.clone() for t in base) for _ in range(LAYERS)]  # LAYERS calls per graph
+            del base
             row = {"heads": heads, "kv_heads": 2, "steps": steps, "q_offset": pos0}
             for key, split in (("us_split", True), ("us_unsplit", False)):
                 row[key] = 1e3 * time_graph(
-                    torch, lambda: backend.attention_prefill(qc, kc, vc, 256**-0.5, torch.bfloat16,
-                                                             q_offset=pos0, split_keys=split),
-                    max(20, esteps // 10), 5)
+                    torch, lambda: [backend.attention_prefill(qc, kc, vc, 256**-0.5, torch.bfloat16,
+                                                              q_offset=pos0, split_keys=split)
+                                    for qc, kc, vc in sets],
+                    max(20, esteps // 10), 5) / LAYERS
             if pos0 > 0:
                 # steady state of a chunk loop with the images kept (only this chunk's blocks converted)
-                imgs = backend.prefill_images(pos0 + steps, 2, 256)
+                imgs = [backend.prefill_images(pos0 + steps, 2, 256) for _ in sets]
                 row["us_split_kept_images"] = 1e3 * time_graph(
-                    torch, lambda: backend.attention_prefill(qc, kc, vc, 256**-0.5, torch.bfloat16,
-                                                             q_offset=pos0, images=imgs),
-                    max(20, esteps // 10), 5)
+                    torch, lambda: [backend.attention_prefill(qc, kc, vc, 256**-0.5, torch.bfloat16,
+                                                              q_offset=pos0, images=im)
+                                    for (qc, kc, vc), im in zip(sets, imgs)],
+                    max(20, esteps // 10), 5) / LAYERS
                 del imgs
+            del sets
             fl = 2 * heads * 256 * steps * (steps + 2 * pos0 + 1)
             row["TFLOPs_split"] = fl / (row["us_split"] * 1e-6) / 1e12
             chunked.append(row)
