@@ -77,10 +77,6 @@ __device__ __forceinline__ bf16x8 lds_read_tr_pair(const BT_LDS uint16_t* p0, co
 // operand canonicalisation fmaxf needs in IEEE mode (-inf stays the identity).
 __device__ __forceinline__ float fmax_nc(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
-__device__ __forceinline__ float wave_max_xor(float x, int mask) {
-  return fmaxf(x, __shfl_xor(x, mask, 64));
-}
-
 // Max / sum of x over lanes l and l ^ 32 with one v_permlane32_swap (gfx950):
 // swapping the upper half of one copy with the lower half of another leaves
 // {x[0..31], x[0..31]} and {x[32..63], x[32..63]}.
@@ -93,6 +89,20 @@ __device__ __forceinline__ float halves_max(float x) {
 __device__ __forceinline__ float rows16_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmax_nc(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Sum of x over lanes l and l ^ 16 (v_permlane16_swap, as rows16_max).
+__device__ __forceinline__ float rows16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// fmaxf (NaN-ignoring) of x over lanes l and l ^ 16 / l ^ 32, without an LDS round trip.
+__device__ __forceinline__ float rows16_fmaxf(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_fmaxf(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float halves_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -338,8 +338,8 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
       x[j] = tile * 16 + kg * 4 + j < valid ? vv : -INFINITY;
     }
     float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    tmax = wave_max_xor(tmax, 16);
-    tmax = wave_max_xor(tmax, 32);
+    tmax = rows16_fmaxf(tmax);  // the column's four lane groups (VALU lane swaps)
+    tmax = halves_fmaxf(tmax);
     // Lazy reference max: m_run moves only when a score exceeds it by more
     // than 2^8 (log2 domain), so p <= 2^8 and O / l are rescaled only then --
     // behind a wave-uniform branch, almost never after the first tile.  The
@@ -383,8 +383,7 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   }
 
   // ---- wave epilogue: full row sums, hi + lo merge ---------------------------
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = halves_sum(rows16_sum(l_run));
 #pragma unroll
   for (int dt = 0; dt < kDTiles; ++dt) {
 #pragma unroll
@@ -421,21 +420,28 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   for (int item = threadIdx.x; item < G * (D / 4); item += kThreads) {
     const int h = item / (D / 4);
     const int d = (item % (D / 4)) * 4;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < W; ++w) mx = fmaxf(mx, mm[w * GMAX + h]);
-    float lsum = 0.f;
-    float4 acc = {0.f, 0.f, 0.f, 0.f};
-    // Branch-free, so all LDS reads are in flight together.  A wave without
-    // valid tokens has l = 0, m = -inf and a zero partial: its weight is 0.
+    // Every LDS read is issued before the first use and the weights are a
+    // select, not a branch (a branch per wave made each l read its own LDS
+    // round trip).  A wave without valid tokens has l = 0, m = -inf and a zero
+    // partial: its weight is 0 (the exp2 of its NaN difference is discarded).
+    float mw[W], lw[W];
     float4 ow[W];
 #pragma unroll
-    for (int w = 0; w < W; ++w) ow[w] = *reinterpret_cast<const float4*>(mlds + (w * GMAX + h) * kMoStride + d);
+    for (int w = 0; w < W; ++w) {
+      mw[w] = mm[w * GMAX + h];
+      lw[w] = ml[w * GMAX + h];
+      ow[w] = *reinterpret_cast<const float4*>(mlds + (w * GMAX + h) * kMoStride + d);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, mw[w]);
+    float lsum = 0.f;
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float lw = ml[w * GMAX + h];
-      const float sc = lw > 0.f ? fast_exp2(mm[w * GMAX + h] - mx) : 0.f;
-      lsum += lw * sc;
+      const float e = fast_exp2(mw[w] - mx);
+      const float sc = lw[w] > 0.f ? e : 0.f;
+      lsum += lw[w] * sc;
       acc.x += ow[w].x * sc; acc.y += ow[w].y * sc; acc.z += ow[w].z * sc; acc.w += ow[w].w * sc;
     }
     const int64_t row = (int64_t)(head0 + h) * p.total_splits + split_idx;
