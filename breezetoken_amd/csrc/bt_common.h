@@ -109,6 +109,40 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// x op x[l ^ MASK] for one butterfly step, without an LDS round trip: DPP for
+// MASK 1 and 2 (quad permutes) and 4 and 8 (row shifts, the two halves of each
+// pair of banks taking opposite directions), lane swaps for 16 and 32.  Each
+// step is one commutative two-operand op, so the result equals
+// op(x, __shfl_xor(x, MASK)) bit for bit.
+template <int MASK>
+__device__ __forceinline__ float xor_partner(float x) {
+  const int v = __float_as_int(x);
+  if constexpr (MASK == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+  if constexpr (MASK == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+  if constexpr (MASK == 4) {  // banks 0, 2 read lane + 4 (row_shl:4), banks 1, 3 lane - 4 (row_shr:4)
+    const int lo = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0x5, false);
+    return __int_as_float(__builtin_amdgcn_update_dpp(lo, v, 0x114, 0xf, 0xA, false));
+  }
+  if constexpr (MASK == 8) {  // banks 0, 1 read lane + 8 (row_shl:8), banks 2, 3 lane - 8 (row_shr:8)
+    const int lo = __builtin_amdgcn_update_dpp(0, v, 0x108, 0xf, 0x3, false);
+    return __int_as_float(__builtin_amdgcn_update_dpp(lo, v, 0x118, 0xf, 0xC, false));
+  }
+  static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "xor_partner: 1, 2, 4 or 8");
+  return x;
+}
+template <int MASK>
+__device__ __forceinline__ float xor_sum(float x) {
+  if constexpr (MASK == 16) return rows16_sum(x);
+  else if constexpr (MASK == 32) return halves_sum(x);
+  else return x + xor_partner<MASK>(x);
+}
+template <int MASK>
+__device__ __forceinline__ float xor_fmaxf(float x) {
+  if constexpr (MASK == 16) return rows16_fmaxf(x);
+  else if constexpr (MASK == 32) return halves_fmaxf(x);
+  else return fmaxf(x, xor_partner<MASK>(x));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

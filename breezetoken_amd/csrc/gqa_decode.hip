@@ -459,8 +459,22 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
 namespace {
 
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  x = xor_fmaxf<32>(x);
+  x = xor_fmaxf<16>(x);
+  x = xor_fmaxf<8>(x);
+  x = xor_fmaxf<4>(x);
+  x = xor_fmaxf<2>(x);
+  return xor_fmaxf<1>(x);
+}
+// Sum over the lane bits at and above log2(FROM) (a butterfly from FROM to 32).
+template <int FROM>
+__device__ __forceinline__ float sum_from(float x) {
+  if constexpr (FROM <= 1) x = xor_sum<1>(x);
+  if constexpr (FROM <= 2) x = xor_sum<2>(x);
+  if constexpr (FROM <= 4) x = xor_sum<4>(x);
+  if constexpr (FROM <= 8) x = xor_sum<8>(x);
+  if constexpr (FROM <= 16) x = xor_sum<16>(x);
+  if constexpr (FROM <= 32) x = xor_sum<32>(x);
   return x;
 }
 
@@ -539,14 +553,11 @@ __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p)
   }
   // Sum over the split groups (the lane bits above the column); every float4 column sees the
   // same splits, so each column's wsum is the full weight sum.
-#pragma unroll
-  for (int o = kCols; o < 64; o <<= 1) {
-    acc.x += __shfl_xor(acc.x, o, 64);
-    acc.y += __shfl_xor(acc.y, o, 64);
-    acc.z += __shfl_xor(acc.z, o, 64);
-    acc.w += __shfl_xor(acc.w, o, 64);
-    wsum += __shfl_xor(wsum, o, 64);
-  }
+  acc.x = sum_from<kCols>(acc.x);
+  acc.y = sum_from<kCols>(acc.y);
+  acc.z = sum_from<kCols>(acc.z);
+  acc.w = sum_from<kCols>(acc.w);
+  wsum = sum_from<kCols>(wsum);
   if (t < kCols) {
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
     acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
