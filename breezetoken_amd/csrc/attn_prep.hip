@@ -34,11 +34,7 @@ __device__ __forceinline__ T uniform_load_prep(const T* p) {
   return ((const __attribute__((address_space(4))) T*)(p))[0];
 }
 
-__device__ __forceinline__ float wave_sum_prep(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-  return x;
-}
+__device__ __forceinline__ float wave_sum_prep(float x) { return wave_sum(x); }
 
 // Normalise and rotate the D values a wave holds (lane l: d = l*E .. l*E+E-1).
 template <int D>

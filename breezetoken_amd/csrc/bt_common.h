@@ -109,38 +109,81 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// x op x[l ^ MASK] for one butterfly step, without an LDS round trip: DPP for
-// MASK 1 and 2 (quad permutes) and 4 and 8 (row shifts, the two halves of each
-// pair of banks taking opposite directions), lane swaps for 16 and 32.  Each
-// step is one commutative two-operand op, so the result equals
-// op(x, __shfl_xor(x, MASK)) bit for bit.
+// op(x, x[l ^ MASK]) for one butterfly step of a commutative op on 32-bit
+// lanes, without an LDS round trip: DPP for MASK 1 and 2 (quad permutes) and
+// 4 and 8 (row shifts, the two halves of each pair of banks taking opposite
+// directions), lane swaps for 16 and 32.  The op sees the lane's own value and
+// its partner's, so the result equals op(x, __shfl_xor(x, MASK)) bit for bit.
 template <int MASK>
-__device__ __forceinline__ float xor_partner(float x) {
-  const int v = __float_as_int(x);
-  if constexpr (MASK == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
-  if constexpr (MASK == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+__device__ __forceinline__ uint32_t xor_partner_bits(uint32_t x) {
+  const int v = (int)x;
+  if constexpr (MASK == 1) return (uint32_t)__builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
+  if constexpr (MASK == 2) return (uint32_t)__builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false);  // quad_perm 2,3,0,1
   if constexpr (MASK == 4) {  // banks 0, 2 read lane + 4 (row_shl:4), banks 1, 3 lane - 4 (row_shr:4)
     const int lo = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0x5, false);
-    return __int_as_float(__builtin_amdgcn_update_dpp(lo, v, 0x114, 0xf, 0xA, false));
+    return (uint32_t)__builtin_amdgcn_update_dpp(lo, v, 0x114, 0xf, 0xA, false);
   }
   if constexpr (MASK == 8) {  // banks 0, 1 read lane + 8 (row_shl:8), banks 2, 3 lane - 8 (row_shr:8)
     const int lo = __builtin_amdgcn_update_dpp(0, v, 0x108, 0xf, 0x3, false);
-    return __int_as_float(__builtin_amdgcn_update_dpp(lo, v, 0x118, 0xf, 0xC, false));
+    return (uint32_t)__builtin_amdgcn_update_dpp(lo, v, 0x118, 0xf, 0xC, false);
   }
-  static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "xor_partner: 1, 2, 4 or 8");
+  static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "xor_partner_bits: 1, 2, 4 or 8");
   return x;
 }
-template <int MASK>
-__device__ __forceinline__ float xor_sum(float x) {
-  if constexpr (MASK == 16) return rows16_sum(x);
-  else if constexpr (MASK == 32) return halves_sum(x);
-  else return x + xor_partner<MASK>(x);
+template <int MASK, typename Op>
+__device__ __forceinline__ uint32_t xor_op(uint32_t x, Op op) {
+  if constexpr (MASK == 16 || MASK == 32) {
+    const auto r = MASK == 16 ? __builtin_amdgcn_permlane16_swap(x, x, false, false)
+                              : __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return op(r[0], r[1]);  // the lane's own value and its partner's
+  } else {
+    return op(x, xor_partner_bits<MASK>(x));
+  }
 }
+struct OpFAdd {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return __float_as_uint(__uint_as_float(a) + __uint_as_float(b)); }
+};
+struct OpFMaxf {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b))); }
+};
+struct OpUMax {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+};
+struct OpIAdd {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return (uint32_t)((int)a + (int)b); }
+};
+struct OpIMax {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return (int)a > (int)b ? a : b; }
+};
 template <int MASK>
-__device__ __forceinline__ float xor_fmaxf(float x) {
-  if constexpr (MASK == 16) return rows16_fmaxf(x);
-  else if constexpr (MASK == 32) return halves_fmaxf(x);
-  else return fmaxf(x, xor_partner<MASK>(x));
+__device__ __forceinline__ float xor_sum(float x) { return __uint_as_float(xor_op<MASK>(__float_as_uint(x), OpFAdd{})); }
+template <int MASK>
+__device__ __forceinline__ float xor_fmaxf(float x) { return __uint_as_float(xor_op<MASK>(__float_as_uint(x), OpFMaxf{})); }
+template <int MASK>
+__device__ __forceinline__ uint32_t xor_umax(uint32_t x) { return xor_op<MASK>(x, OpUMax{}); }
+// Whole-wave butterflies, masks 32, 16, ..., 1 in that order (every lane gets the result).
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_op_desc(uint32_t x, Op op) {
+  x = xor_op<32>(x, op);
+  x = xor_op<16>(x, op);
+  x = xor_op<8>(x, op);
+  x = xor_op<4>(x, op);
+  x = xor_op<2>(x, op);
+  return xor_op<1>(x, op);
+}
+__device__ __forceinline__ float wave_sum(float x) { return __uint_as_float(wave_op_desc(__float_as_uint(x), OpFAdd{})); }
+__device__ __forceinline__ float wave_fmaxf(float x) { return __uint_as_float(wave_op_desc(__float_as_uint(x), OpFMaxf{})); }
+__device__ __forceinline__ uint32_t wave_umax(uint32_t x) { return wave_op_desc(x, OpUMax{}); }
+// Sum over the lane bits at and above log2(FROM), masks FROM, 2 FROM, ..., 32.
+template <int FROM>
+__device__ __forceinline__ float sum_from(float x) {
+  if constexpr (FROM <= 1) x = xor_sum<1>(x);
+  if constexpr (FROM <= 2) x = xor_sum<2>(x);
+  if constexpr (FROM <= 4) x = xor_sum<4>(x);
+  if constexpr (FROM <= 8) x = xor_sum<8>(x);
+  if constexpr (FROM <= 16) x = xor_sum<16>(x);
+  if constexpr (FROM <= 32) x = xor_sum<32>(x);
+  return x;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -38,11 +38,7 @@ struct GdnShape {
   static_assert(kRows >= 1 && D % kChunks == 0, "row chunks tile the key rows");
 };
 
-__device__ __forceinline__ float wave_sum_gdn(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-  return x;
-}
+__device__ __forceinline__ float wave_sum_gdn(float x) { return wave_sum(x); }
 
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
   return float4{a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
@@ -53,13 +49,10 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) {
 // across the waves through LDS.  Every thread returns the total of its group.
 template <typename S>
 __device__ __forceinline__ float4 sum_over_rows(float4 v, float4* red) {
-#pragma unroll
-  for (int o = S::kCols; o < 64; o <<= 1) {
-    v.x += __shfl_xor(v.x, o, 64);
-    v.y += __shfl_xor(v.y, o, 64);
-    v.z += __shfl_xor(v.z, o, 64);
-    v.w += __shfl_xor(v.w, o, 64);
-  }
+  v.x = sum_from<S::kCols>(v.x);
+  v.y = sum_from<S::kCols>(v.y);
+  v.z = sum_from<S::kCols>(v.z);
+  v.w = sum_from<S::kCols>(v.w);
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   if (lane < S::kCols) red[wave * S::kCols + lane] = v;

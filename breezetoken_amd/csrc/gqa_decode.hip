@@ -458,25 +458,7 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
 
 namespace {
 
-__device__ __forceinline__ float wave_max(float x) {
-  x = xor_fmaxf<32>(x);
-  x = xor_fmaxf<16>(x);
-  x = xor_fmaxf<8>(x);
-  x = xor_fmaxf<4>(x);
-  x = xor_fmaxf<2>(x);
-  return xor_fmaxf<1>(x);
-}
-// Sum over the lane bits at and above log2(FROM) (a butterfly from FROM to 32).
-template <int FROM>
-__device__ __forceinline__ float sum_from(float x) {
-  if constexpr (FROM <= 1) x = xor_sum<1>(x);
-  if constexpr (FROM <= 2) x = xor_sum<2>(x);
-  if constexpr (FROM <= 4) x = xor_sum<4>(x);
-  if constexpr (FROM <= 8) x = xor_sum<8>(x);
-  if constexpr (FROM <= 16) x = xor_sum<16>(x);
-  if constexpr (FROM <= 32) x = xor_sum<32>(x);
-  return x;
-}
+
 
 }  // namespace
 
@@ -528,7 +510,7 @@ __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p)
 #pragma unroll
   for (int i = 1; i < kPre; ++i) mx = fmaxf(mx, pl[i]);
   for (int s = sg + GROUPS * kPre; s < ns; s += GROUPS) mx = fmaxf(mx, lse[s]);
-  mx = wave_max(mx);
+  mx = wave_fmaxf(mx);
   // Empty splits have lse = -inf: weight 0, and their (never written) partial is skipped.
   const float m_use = mx == -INFINITY ? 0.f : mx;
 

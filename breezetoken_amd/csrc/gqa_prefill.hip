@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void gqa_prefill_kernel(PrefillPara
       const int qrow = min(q0 + qcol, S - 1);
       const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + kgrp * 8;
       const int eq = q_row_f16(p.q, p.q_f32 != 0, off, 16, qop, [](uint32_t mx) {
-        return max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));  // the row's two lane halves
+        return xor_umax<32>(mx);  // the row's two lane halves
       });
       c_col = __builtin_ldexpf(p.scale_log2, eq);
     }

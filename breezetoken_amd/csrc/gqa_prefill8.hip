@@ -259,8 +259,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       const int qrow = min(q0 + i16, S - 1);
       const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + g4 * 8;
       const int eq = q_row_f16(p.q, p.q_f32 != 0, off, 32, qop, [](uint32_t mx) {
-        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
-        return max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+        return xor_umax<32>(xor_umax<16>(mx));  // the row's four lane groups
       });
       c_col = __builtin_ldexpf(p.scale_log2, eq);
     }
@@ -280,8 +279,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
                 mx[b] = max(mx[b], max(draw[b][j][i] & 0x7fffu, (draw[b][j][i] >> 16) & 0x7fffu));
   #pragma unroll
       for (int b = 0; b < 2; ++b) {
-  #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx[b] = max(mx[b], (uint32_t)__shfl_xor((int)mx[b], o, 64));
+        mx[b] = wave_umax(mx[b]);
         if (lane == 0) dmax[b][wave] = mx[b];
       }
       __syncthreads();
@@ -400,7 +398,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   #pragma unroll
         for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[sub][r]);
       const float c_log2 = __builtin_ldexpf(c_col, ek);  // with the K block's scale
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = xor_fmaxf<16>(tmax);
       tmax = halves_max(tmax) * c_log2;
       const bool move = tmax > m_ref + kLazy8;
       const float m_new = move ? tmax : m_ref;
@@ -494,7 +492,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     if ((last - kb0) & 1) pv(Buf8<1>{}, pk); else pv(Buf8<0>{}, pk);
 
     // ---- epilogue: row sums over the four lane groups, normalise, store -------
-    l_run += __shfl_xor(l_run, 16, 64);
+    l_run = xor_sum<16>(l_run);
     l_run = halves_sum(l_run);
     if (nchunks > 1) {
       // One chunk of a split query block: normalised partial and LSE of row

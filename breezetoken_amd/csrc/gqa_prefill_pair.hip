@@ -192,8 +192,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // raw values take the registers O frees between blocks), then each row's
   // largest |q| is reduced over its four lane groups and the values converted.
   auto row_scale = [&](int t, uint32_t mx) {
-    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));  // the row's four lane groups
-    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+    mx = xor_umax<32>(xor_umax<16>(mx));  // the row's four lane groups
     const int eq = absmax_exp(mx);
     c_col[t] = __builtin_ldexpf(p.scale_log2, eq);
     return eq;
@@ -299,7 +298,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   auto row_sums = [&](float (&lsum)[NQT]) {
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
-      float l = l_run[t] + __shfl_xor(l_run[t], 16, 64);
+      float l = xor_sum<16>(l_run[t]);
       lsum[t] = halves_sum(l);
     }
   };

@@ -83,8 +83,7 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) kmx = max(kmx, max(krow[j][i] & 0x7fffu, (krow[j][i] >> 16) & 0x7fffu));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, o, 64));
+    kmx = wave_umax(kmx);
     if ((threadIdx.x & 63) == 0) wmax[1][threadIdx.x >> 6] = kmx;
     __syncthreads();
     kmx = max(max(wmax[1][0], wmax[1][1]), max(wmax[1][2], wmax[1][3]));
@@ -120,8 +119,7 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
       for (int i = 0; i < 4; ++i) mx = max(mx, max(rows[j][i] & 0x7fffu, (rows[j][i] >> 16) & 0x7fffu));
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+  mx = wave_umax(mx);
   if ((threadIdx.x & 63) == 0) wmax[0][threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = max(max(wmax[0][0], wmax[0][1]), max(wmax[0][2], wmax[0][3]));

@@ -29,11 +29,7 @@ __device__ __forceinline__ int plan_splits(int len, int cap) {
 // Sum (or max) over the work-group; every thread gets the result.
 template <bool MAX>
 __device__ int block_reduce(int x, int* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const int y = __shfl_xor(x, o, 64);
-    x = MAX ? (x > y ? x : y) : x + y;
-  }
+  x = MAX ? (int)wave_op_desc((uint32_t)x, OpIMax{}) : (int)wave_op_desc((uint32_t)x, OpIAdd{});
   const int wave = threadIdx.x >> 6;
   __syncthreads();  // red may still be read from the previous call
   if ((threadIdx.x & 63) == 0) red[wave] = x;
