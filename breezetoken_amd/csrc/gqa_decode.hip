@@ -445,14 +445,14 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
       acc.x += ow[w].x * sc; acc.y += ow[w].y * sc; acc.z += ow[w].z * sc; acc.w += ow[w].w * sc;
     }
     const int64_t row = (int64_t)(head0 + h) * p.total_splits + split_idx;
-    if (lsum > 0.f) {
-      const float inv = 1.f / lsum;
-      acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
-      *reinterpret_cast<float4*>(p.part + row * D + d) = acc;
-      if (d == 0) p.lse[row] = fast_log2(lsum) + mx;
-    } else if (d == 0) {
-      p.lse[row] = -INFINITY;
-    }
+    // The partial is stored unconditionally (zeros for a split without valid
+    // tokens, whose lse of -inf the combine skips), so the compiler cannot
+    // sink its LDS reads behind the weights' into a second round trip.
+    const bool has = lsum > 0.f;
+    const float inv = has ? 1.f / lsum : 0.f;
+    acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
+    *reinterpret_cast<float4*>(p.part + row * D + d) = acc;
+    if (d == 0) p.lse[row] = has ? fast_log2(lsum) + mx : -INFINITY;
   }
 }
 
