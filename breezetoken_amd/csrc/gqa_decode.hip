@@ -261,11 +261,6 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   const int tstride = ns_eff * W;                       // tile distance between a wave's steps
   const int tfirst = s + ns_eff * wave;                 // this wave's first tile
   const int my_tiles = tfirst < tiles ? (tiles - tfirst + tstride - 1) / tstride : 0;
-  if (my_tiles > 0 && !spec_loaded) {
-    issue_k(tfirst);
-    issue_v(tfirst);
-  }
-
   // ---- Q^T operand (bf16 hi or lo of q*scale*log2e): wave w builds d-step w.
   if (wave < kSteps) {
     float qv[8];
@@ -292,6 +287,15 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
     }
     qlds[wave * 64 + lane] = u32x4{pack2(h16[0], h16[1]), pack2(h16[2], h16[3]), pack2(h16[4], h16[5]),
                                    pack2(h16[6], h16[7])};
+  }
+  // The first tile's loads go out after the Q^T build: issued before it, they
+  // would sit behind q in the wave's load queue on one path and not on the
+  // other (a wave without tiles), and the compiler's wait for q would then be
+  // for every load -- the wave's first tile, and through the barrier the
+  // slowest wave's.  q and pos arrive about together, so this costs little.
+  if (my_tiles > 0 && !spec_loaded) {
+    issue_k(tfirst);
+    issue_v(tfirst);
   }
   // Publish Q^T without waiting for the K/V requests in flight (no vmcnt wait).
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
