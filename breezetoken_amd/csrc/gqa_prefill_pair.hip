@@ -393,16 +393,26 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       __builtin_amdgcn_sched_barrier(0);
     }
     // Causal mask: key key0 + kt*16 + g4*4 + r against this column's position.
+    // The lane's column and lane group are re-derived here from the V^T
+    // operand address (g4 * D * 16 + i16 * 16), which the loop keeps anyway,
+    // through an opaque copy: kept live across the key loop instead, the
+    // column index was spilled, and its reload each step -- a scratch load,
+    // counted with the tile copies -- made the softmax wait for every copy in
+    // flight before reusing the register.
+    uint32_t va = vaddr;
+    asm volatile("" : "+v"(va));
+    const int col = (int)((va >> 4) & 15u);
+    const int grp = (int)(va / (uint32_t)(D * 16));
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
       const int qpos = P0 + blk * sh.pos + poff[t];  // first position of the q-tile
       if (key0 + kUnit - 1 > qpos) {
-        const int mypos = qpos + i16;
+        const int mypos = qpos + col;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (key0 + kt * 16 + g4 * 4 + r > mypos) sacc[kt][t][r] = -INFINITY;
+            if (key0 + kt * 16 + grp * 4 + r > mypos) sacc[kt][t][r] = -INFINITY;
       }
     }
     // The V^T tile's scale: e of its 64-key block (wave-uniform).  P enters
