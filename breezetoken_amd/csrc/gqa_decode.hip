@@ -106,8 +106,10 @@ enum DecodeMode : int {
 //
 // Per tile and wave, K (16 tokens x D) and V land in registers; K feeds the
 // MFMA directly, V is staged through the wave's XOR-swizzled LDS tile and read
-// back transposed.  A wave requests its next K as soon as Q.K^T has consumed
-// the current one and its next V as soon as the current V is in LDS.
+// back transposed.  A wave requests its next V as soon as the current V is in
+// LDS, and its next K as soon as Q.K^T has consumed the current one -- except
+// after the first tile, where the next K goes out with the next V.  A wave's
+// first tile is requested after its slice of Q^T is built (wave 0's, at entry).
 template <int GMAX, int D, int W, int MODE, bool QBF16>
 __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplitParams p) {
   constexpr int kThreads = W * 64;
