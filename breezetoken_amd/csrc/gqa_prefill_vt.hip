@@ -53,7 +53,12 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
   static_assert(kItems <= 256, "one item per thread");
   static_assert(kPrefillKeyBlock * kDC % 256 == 0, "whole K units per thread");
   constexpr int kBlk = kPrefillKeyBlock;
-  const int blk = p.img_first + (int)blockIdx.x, g = blockIdx.y;
+  // The kv heads of a block are neighbours in the grid's x (work-group x =
+  // block * Hkv + head): both read the same token-major cache rows, one half
+  // each, and dispatched together they do so at about the same time, which the
+  // DRAM serves better (C4 S = 8192 about -3 us per call against one grid row
+  // per head).
+  const int blk = p.img_first + (int)blockIdx.x / p.kv_heads, g = (int)blockIdx.x % p.kv_heads;
   const int nblk = p.img_blocks;  // image layout stride per kv head
   const uint32_t row_bytes = (uint32_t)(p.kv_stride_tok * 2);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -158,7 +163,7 @@ hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, int order, h
   if (order != kVtOrder16 && order != kVtOrder32) return hipErrorInvalidValue;
   if (p.img_blocks < nblk || p.img_first < 0 || p.img_first > nblk) return hipErrorInvalidValue;
   if (p.img_first == nblk) return hipSuccess;  // every block is already in the images
-  const dim3 grid(nblk - p.img_first, p.kv_heads, 2);
+  const dim3 grid((nblk - p.img_first) * p.kv_heads, 1, 2);
   switch (head_dim) {
     case 128:
       if (order == kVtOrder16) hipLaunchKernelGGL((prefill_vts_kernel<128, kVtOrder16>), grid, dim3(256), 0, stream, p);
