@@ -337,7 +337,9 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("this build measures one GPU only: the decode/prefill kernels run on a single "
-              "MI355X and no multi-GPU path is built (see DESIGN.md); run with --gpus 1",
+              "MI355X and no multi-GPU path is built (the kernels shard by kv head or by "
+              "context, with an all-gather of split partials before the same combine); "
+              "run with --gpus 1",
               file=sys.stderr)
         return 2
 
