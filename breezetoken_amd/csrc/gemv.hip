@@ -10,8 +10,9 @@
 //
 // MI355X layout: a work-group of 4 waves owns a tile of 64*VEC columns (VEC
 // consecutive bf16 per lane: one 16- or 8-byte load per row) over one share of
-// K; wave w takes rows k0 + w, k0 + w + 4, ... and keeps kRowsAhead rows of
-// loads in flight, so every byte of W is streamed once with non-temporal
+// K; wave w takes rows k0 + w, k0 + w + 4, ... and keeps ROWS rows of loads in
+// flight (16 when that covers a whole share of at most 64 rows in one round
+// trip, else 8), so every byte of W is streamed once with non-temporal
 // buffer loads (rows are contiguous segments of 64*VEC*2 bytes; the buffer
 // range check turns loads past the matrix into zeros).  x[k] is wave-uniform
 // and read through the scalar cache.  The four waves' accumulators are summed
@@ -28,7 +29,6 @@ namespace bt {
 namespace {
 
 constexpr int kGemvWaves = 4;
-constexpr int kRowsAhead = 8;
 
 template <typename T>
 __device__ __forceinline__ T uniform_load_gemv(const T* p, int i) {
@@ -64,7 +64,7 @@ __device__ __forceinline__ void fma_row(float (&acc)[VEC], const typename GemvLo
 
 }  // namespace
 
-template <int VEC>
+template <int VEC, int ROWS>
 __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams p) {
   constexpr int kTile = 64 * VEC;
   __shared__ float red[kGemvWaves][kTile];
@@ -85,15 +85,15 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams p) {
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
 
-  // Rows k0 + wave + 4*j; kRowsAhead loads in flight per pass.
+  // Rows k0 + wave + 4*j; ROWS loads in flight per pass.
   int k = k0 + wave;
-  for (; k + kGemvWaves * (kRowsAhead - 1) < k1; k += kGemvWaves * kRowsAhead) {
-    typename GemvLoad<VEC>::type wv[kRowsAhead];
+  for (; k + kGemvWaves * (ROWS - 1) < k1; k += kGemvWaves * ROWS) {
+    typename GemvLoad<VEC>::type wv[ROWS];
 #pragma unroll
-    for (int j = 0; j < kRowsAhead; ++j)
+    for (int j = 0; j < ROWS; ++j)
       wv[j] = GemvLoad<VEC>::load(wrs, (uint32_t)((k + kGemvWaves * j) * p.ldw) * 2 + col_off);
 #pragma unroll
-    for (int j = 0; j < kRowsAhead; ++j) fma_row<VEC>(acc, wv[j], uniform_load_gemv(p.x, k + kGemvWaves * j));
+    for (int j = 0; j < ROWS; ++j) fma_row<VEC>(acc, wv[j], uniform_load_gemv(p.x, k + kGemvWaves * j));
   }
   for (; k < k1; k += kGemvWaves) {
     const typename GemvLoad<VEC>::type wv = GemvLoad<VEC>::load(wrs, (uint32_t)(k * p.ldw) * 2 + col_off);
@@ -113,34 +113,52 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams p) {
   }
 }
 
-// y[n] = sum over shares s = 0 .. SK-1 of partial[s][n], in that order; eight
-// shares' loads are issued before their adds.
+// y[n] = sum over shares s = 0 .. SK-1 of partial[s][n], in that order.  The
+// loads of BATCH shares are issued before their adds (one memory round trip
+// for SK <= BATCH) without a branch per load: they go through a buffer
+// descriptor that ends at the last share, so a load past it reads zero, and
+// only the adds of the shares that exist are kept.  BATCH is the smallest of
+// 8, 16, 32, 64 that holds SK (64 beyond): loads past the last share still
+// cost issue time (BATCH 64 at SK = 16: +0.7 us).
+template <int BATCH>
 __global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvParams p) {
   const int n = blockIdx.x * 256 + threadIdx.x;
   if (n >= p.N) return;
-  const float* col = p.partial + n;
+  // splits * N * 4 < 2^31 (at most ~1.5 MB for the shapes gemv_shape splits).
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc(p.partial, (short)0, p.splits * p.N * 4, 0x00020000);
+  const uint32_t share_bytes = (uint32_t)p.N * 4;
   float v = 0.f;
-  int sh = 0;
-  for (; sh + 8 <= p.splits; sh += 8) {
-    float t[8];
+  for (int sh = 0; sh < p.splits; sh += BATCH) {
+    const int cnt = min(BATCH, p.splits - sh);
+    float t[BATCH];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t[j] = col[(int64_t)(sh + j) * p.N];
+    for (int j = 0; j < BATCH; ++j)
+      t[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           prs, (int)((uint32_t)(sh + j) * share_bytes + (uint32_t)n * 4), 0, 0));
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v += t[j];
+    for (int j = 0; j < BATCH; ++j)
+      if (j < cnt) v += t[j];
   }
-  for (; sh < p.splits; ++sh) v += col[(int64_t)sh * p.N];
   p.y[n] = v;
 }
 
 hipError_t launch_gemv(const GemvParams& p, int vec, hipStream_t stream) {
   const int tile = 64 * vec;
   const dim3 grid((p.N + tile - 1) / tile, p.splits);
-  if (vec == 8) hipLaunchKernelGGL(gemv_bf16_kernel<8>, grid, dim3(256), 0, stream, p);
-  else if (vec == 4) hipLaunchKernelGGL(gemv_bf16_kernel<4>, grid, dim3(256), 0, stream, p);
+  const bool one_pass = (p.K + p.splits - 1) / p.splits <= 64;  // a share's rows in one batch of 16
+  if (vec == 8 && one_pass) hipLaunchKernelGGL((gemv_bf16_kernel<8, 16>), grid, dim3(256), 0, stream, p);
+  else if (vec == 8) hipLaunchKernelGGL((gemv_bf16_kernel<8, 8>), grid, dim3(256), 0, stream, p);
+  else if (vec == 4 && one_pass) hipLaunchKernelGGL((gemv_bf16_kernel<4, 16>), grid, dim3(256), 0, stream, p);
+  else if (vec == 4) hipLaunchKernelGGL((gemv_bf16_kernel<4, 8>), grid, dim3(256), 0, stream, p);
   else return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
-  hipLaunchKernelGGL(gemv_reduce_kernel, dim3((p.N + 255) / 256), dim3(256), 0, stream, p);
+  const dim3 rgrid((p.N + 255) / 256);
+  if (p.splits <= 8) hipLaunchKernelGGL(gemv_reduce_kernel<8>, rgrid, dim3(256), 0, stream, p);
+  else if (p.splits <= 16) hipLaunchKernelGGL(gemv_reduce_kernel<16>, rgrid, dim3(256), 0, stream, p);
+  else if (p.splits <= 32) hipLaunchKernelGGL(gemv_reduce_kernel<32>, rgrid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL(gemv_reduce_kernel<64>, rgrid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

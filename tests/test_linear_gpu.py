@@ -28,10 +28,14 @@ def _check(hip_backend, K, N, seed, ldw=None):
 
 
 @pytest.mark.parametrize("K,N", [(1024, 1024), (1024, 5120), (2048, 1024), (1024, 7168), (3584, 1024),
-                                 (1024, 6144), (1024, 16), (1024, 1000), (96, 72), (4096, 4096)])
+                                 (1024, 6144), (1024, 16), (1024, 1000), (96, 72), (4096, 4096),
+                                 (448, 1024), (1536, 1024), (4160, 512), (8192, 1024), (32768, 512)])
 def test_linear_matches_f32_definition(hip_backend, K, N):
     """(1024, 1024) is the reference test; the others are the 0.8B decode
-    projections (qkv, o, gate|up, down, GDN qkv, beta/alpha) and ragged sizes."""
+    projections (qkv, o, gate|up, down, GDN qkv, beta/alpha) and ragged sizes.
+    The last five reach the split-K reduction's other batch shapes: 7, 24, 65,
+    128 and 256 shares of K (one partial batch of 8 or 32 loads, a full batch of
+    64 plus a remainder, two and four full batches)."""
     _check(hip_backend, K, N, seed=K + N)
 
 
