@@ -11,8 +11,8 @@
 // MI355X layout: a work-group of 4 waves owns a tile of 64*VEC columns (VEC
 // consecutive bf16 per lane: one 16- or 8-byte load per row) over one share of
 // K; wave w takes rows k0 + w, k0 + w + 4, ... and keeps ROWS rows of loads in
-// flight (16 when that covers a whole share of at most 64 rows in one round
-// trip, else 8), so every byte of W is streamed once with non-temporal
+// flight (16 when that covers a whole share of 61..64 rows in one round trip,
+// else 8), so every byte of W is streamed once with non-temporal
 // buffer loads (rows are contiguous segments of 64*VEC*2 bytes; the buffer
 // range check turns loads past the matrix into zeros).  x[k] is wave-uniform
 // and read through the scalar cache.  The four waves' accumulators are summed
@@ -146,7 +146,10 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvParams p) {
 hipError_t launch_gemv(const GemvParams& p, int vec, hipStream_t stream) {
   const int tile = 64 * vec;
   const dim3 grid((p.N + tile - 1) / tile, p.splits);
-  const bool one_pass = (p.K + p.splits - 1) / p.splits <= 64;  // a share's rows in one batch of 16
+  // A share of 61..64 rows is one batch of 16 rows per wave (two batches of 8
+  // otherwise); shorter shares keep 8, so no wave walks them one row at a time.
+  const int k_per = (p.K + p.splits - 1) / p.splits;
+  const bool one_pass = k_per > kGemvWaves * 15 && k_per <= kGemvWaves * 16;
   if (vec == 8 && one_pass) hipLaunchKernelGGL((gemv_bf16_kernel<8, 16>), grid, dim3(256), 0, stream, p);
   else if (vec == 8) hipLaunchKernelGGL((gemv_bf16_kernel<8, 8>), grid, dim3(256), 0, stream, p);
   else if (vec == 4 && one_pass) hipLaunchKernelGGL((gemv_bf16_kernel<4, 16>), grid, dim3(256), 0, stream, p);
