@@ -228,43 +228,25 @@ __device__ __forceinline__ uint32_t pack_f16x2_scaled(float a, float b, int e) {
   return __builtin_bit_cast(uint32_t,
                             __builtin_convertvector((float2_c){__builtin_ldexpf(a, -e), __builtin_ldexpf(b, -e)}, half2_c));
 }
-// One query row's N chunks of 8 values (chunk i at q + off + i * step
-// elements, f32 or bf16) as fp16 MFMA operands scaled by 2^-e, e from the
-// row's largest |q|.  Every load is issued before any is used, so the row
-// costs one memory round trip; `reduce` combines the maxima (as f32 bits of
-// |q|, which order like |q|) of the lanes that share the row.  Returns e.
-template <int N, typename Reduce>
-__device__ __forceinline__ int q_row_f16(const void* q, bool f32, int64_t off, int step, u32x4 (&out)[N],
-                                         Reduce reduce) {
+// Largest |x| of N chunks of 8 f32 values, as the f32 bits of |x| (which order like |x|).
+template <int N>
+__device__ __forceinline__ uint32_t absmax_bits(const float4 (&raw)[N][2]) {
   uint32_t mx = 0;
-  if (f32) {
-    const float* qf = reinterpret_cast<const float*>(q) + off;
-    float4 raw[N][2];
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      raw[i][0] = *reinterpret_cast<const float4*>(qf + (int64_t)i * step);
-      raw[i][1] = *reinterpret_cast<const float4*>(qf + (int64_t)i * step + 4);
+  for (int i = 0; i < N; ++i)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float4 v = raw[i][h];
+      mx = max(mx, max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
+                       max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu)));
     }
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float4 v = raw[i][h];
-        mx = max(mx, max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
-                         max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu)));
-      }
-    const int e = absmax_exp(reduce(mx));
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const float4 a = raw[i][0], b = raw[i][1];
-      out[i] = u32x4{pack_f16x2_scaled(a.x, a.y, e), pack_f16x2_scaled(a.z, a.w, e), pack_f16x2_scaled(b.x, b.y, e),
-                     pack_f16x2_scaled(b.z, b.w, e)};
-    }
-    return e;
-  }
-  const uint16_t* qb = reinterpret_cast<const uint16_t*>(q) + off;
-#pragma unroll
-  for (int i = 0; i < N; ++i) out[i] = *reinterpret_cast<const u32x4*>(qb + (int64_t)i * step);
+  return mx;
+}
+// Raw bf16 chunks in `out` become fp16 scaled by 2^-e, e from the row's
+// largest |q| (`reduce` combines the maxima of the lanes that share the row).
+template <int N, typename Reduce>
+__device__ __forceinline__ int q_bf16_to_f16(u32x4 (&out)[N], Reduce reduce) {
+  uint32_t mx = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
 #pragma unroll
@@ -277,6 +259,76 @@ __device__ __forceinline__ int q_row_f16(const void* q, bool f32, int64_t off, i
                    pack_f16x2_scaled(__uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u), e),
                    pack_f16x2_scaled(__uint_as_float(w[2] << 16), __uint_as_float(w[2] & 0xffff0000u), e),
                    pack_f16x2_scaled(__uint_as_float(w[3] << 16), __uint_as_float(w[3] & 0xffff0000u), e)};
+  }
+  return e;
+}
+// One query row's N chunks of 8 values (chunk i at q + off + i * step
+// elements, f32 or bf16) as fp16 MFMA operands scaled by 2^-e, e from the
+// row's largest |q|.  Every load is issued before any is used, so the row
+// costs one memory round trip; `reduce` combines the maxima (as f32 bits of
+// |q|, which order like |q|) of the lanes that share the row.  Returns e.
+template <int N, typename Reduce>
+__device__ __forceinline__ int q_row_f16(const void* q, bool f32, int64_t off, int step, u32x4 (&out)[N],
+                                         Reduce reduce) {
+  if (f32) {
+    const float* qf = reinterpret_cast<const float*>(q) + off;
+    float4 raw[N][2];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      raw[i][0] = *reinterpret_cast<const float4*>(qf + (int64_t)i * step);
+      raw[i][1] = *reinterpret_cast<const float4*>(qf + (int64_t)i * step + 4);
+    }
+    const int e = absmax_exp(reduce(absmax_bits(raw)));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const float4 a = raw[i][0], b = raw[i][1];
+      out[i] = u32x4{pack_f16x2_scaled(a.x, a.y, e), pack_f16x2_scaled(a.z, a.w, e), pack_f16x2_scaled(b.x, b.y, e),
+                     pack_f16x2_scaled(b.z, b.w, e)};
+    }
+    return e;
+  }
+  const uint16_t* qb = reinterpret_cast<const uint16_t*>(q) + off;
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = *reinterpret_cast<const u32x4*>(qb + (int64_t)i * step);
+  return q_bf16_to_f16(out, reduce);
+}
+
+// f32 q split into two fp16 terms per element: hi = fp16(q * 2^-e) and lo =
+// fp16(q * 2^-e - hi), so hi + lo carries ~22 significant bits and Q.K^T
+// summed over both terms matches f32 q to ~2^-22 relative (hi alone keeps 11
+// bits, and its score error grows with |q|.|k|: at a score standard
+// deviation of 2 it already reaches the 2e-3 output gate).  q * 2^-e - hi is
+// exact in f32.
+__device__ __forceinline__ void split_f16x2(float a, float b, int e, uint32_t& hi, uint32_t& lo) {
+  const float sa = __builtin_ldexpf(a, -e), sb = __builtin_ldexpf(b, -e);
+  const half2_c h = __builtin_convertvector((float2_c){sa, sb}, half2_c);
+  const float ha = (float)h[0], hb = (float)h[1];
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_c){sa - ha, sb - hb}, half2_c));
+}
+// One f32 query row's N chunks of 8 values as hi and lo fp16 operands, in the
+// layout and with the scale of q_row_f16.  Returns e.
+template <int N, typename Reduce>
+__device__ __forceinline__ int q_row_f16_lo(const float* q, int64_t off, int step, u32x4 (&hi)[N], u32x4 (&lo)[N],
+                                            Reduce reduce) {
+  const float* qf = q + off;
+  float4 raw[N][2];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    raw[i][0] = *reinterpret_cast<const float4*>(qf + (int64_t)i * step);
+    raw[i][1] = *reinterpret_cast<const float4*>(qf + (int64_t)i * step + 4);
+  }
+  const int e = absmax_exp(reduce(absmax_bits(raw)));
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float4 a = raw[i][0], b = raw[i][1];
+    uint32_t h[4], l[4];
+    split_f16x2(a.x, a.y, e, h[0], l[0]);
+    split_f16x2(a.z, a.w, e, h[1], l[1]);
+    split_f16x2(b.x, b.y, e, h[2], l[2]);
+    split_f16x2(b.z, b.w, e, h[3], l[3]);
+    hi[i] = u32x4{h[0], h[1], h[2], h[3]};
+    lo[i] = u32x4{l[0], l[1], l[2], l[3]};
   }
   return e;
 }

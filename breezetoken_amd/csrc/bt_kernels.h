@@ -67,6 +67,11 @@ struct PrefillParams {
   int32_t heads;
   int32_t kv_heads;
   int32_t group;       // heads / kv_heads
+  // Two-waves-per-SIMD kernel: the group runs as head_subs subsets of
+  // sub_group heads (sub_group in {1, 2, 4, 8}, the largest power of two
+  // dividing group; grid y = kv_heads x head_subs).
+  int32_t sub_group;
+  int32_t head_subs;
   float scale_log2;
   void* out;
   int out_bf16;
@@ -239,20 +244,19 @@ hipError_t launch_decode_split(const DecodeSplitParams& p, int head_dim, int gri
                                hipStream_t stream);
 hipError_t launch_decode_combine(const CombineParams& p, int head_dim, int heads, int batch,
                                  hipStream_t stream);
-hipError_t launch_prefill(const PrefillParams& p, int head_dim, hipStream_t stream);
-// Two-waves-per-SIMD prefill (gqa_prefill8.hip) for group sizes 1, 2, 4, 8.
+// Two-waves-per-SIMD prefill (gqa_prefill8.hip) for group sizes 1..8: a
+// group runs as subsets of prefill8_sub_group(group) heads.
 bool prefill8_serves(int group, int head_dim);
+int prefill8_sub_group(int group);
 // Pair kernel (gqa_prefill_pair.hip): two query blocks per work-group, 32
 // query columns per wave; group sizes 1, 2, 4, 8.
 bool prefill_pair_serves(int group, int head_dim);
 int prefill_pair_grid(int seqlen, int group, int kv_heads);
 hipError_t launch_prefill_pair(const PrefillParams& p, int head_dim, hipStream_t stream);
 // Scaled fp16 V^T image + per-block exponents (p.vt, p.vexp) in the key order
-// of the 16x16 (kVtOrder16) or 32x32 (kVtOrder32) MFMA result layout, and the
-// scaled fp16 K image + exponents (p.kimg, p.kexp).
-constexpr int kVtOrder16 = 0;
-constexpr int kVtOrder32 = 1;
-hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, int order, hipStream_t stream);
+// of the 16x16 MFMA result layout, and the scaled fp16 K image + exponents
+// (p.kimg, p.kexp).
+hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_row_norm_rope(const RowPrepParams& p, int head_dim, hipStream_t stream);
 hipError_t launch_attn_prep(const RowPrepParams& p, int head_dim, hipStream_t stream);

@@ -128,7 +128,10 @@ bt::PrefillSplitPlan prefill_plan(int32_t seqlen, int32_t q_offset, int32_t head
   const int group = heads / kv_heads;
   if (!bt::prefill8_serves(group, head_dim)) return bt::PrefillSplitPlan{};
   if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim)) return bt::PrefillSplitPlan{};
-  return bt::prefill8_split_plan(seqlen, q_offset, group, kv_heads, head_dim, device_cus());
+  // The kernel runs the group as subsets of sub_group heads, each subset a
+  // row of the grid like a kv head of its own.
+  const int sub = bt::prefill8_sub_group(group);
+  return bt::prefill8_split_plan(seqlen, q_offset, sub, kv_heads * (group / sub), head_dim, device_cus());
 }
 
 }  // namespace
@@ -514,12 +517,13 @@ static int prefill_run(const void* q, int32_t q_dtype, const void* k, const void
   p.keep_images = keep_images ? 1 : 0;
   if (prefill_uses_pair(seqlen, heads, kv_heads, head_dim))
     return hip_rc(bt::launch_prefill_pair(p, head_dim, (hipStream_t)stream));
-  // Group sizes 1, 2, 4, 8 at D = 128 / 256 run two waves per SIMD; other
-  // shapes take the one-wave-per-SIMD kernel (each reads the image order its
-  // MFMA shape needs).  When one work-group per query block would leave CUs
-  // idle or the causal triangle's work is uneven, and `partials` holds the
-  // plan's partials (if it needs any), the key ranges are split.
+  // Every other shape runs two waves per SIMD (groups of 3, 5, 6, 7 as
+  // subsets of 1 or 2 heads).  When one work-group per query block would
+  // leave CUs idle or the causal triangle's work is uneven, and `partials`
+  // holds the plan's partials (if it needs any), the key ranges are split.
   if (bt::prefill8_serves(p.group, head_dim)) {
+    p.sub_group = bt::prefill8_sub_group(p.group);
+    p.head_subs = p.group / p.sub_group;
     int64_t part_offset = 0;
     const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
     if (plan.active() && (!plan.uses_partials() || (partials && partials_bytes >= (int64_t)plan.part_bytes))) {
@@ -533,7 +537,7 @@ static int prefill_run(const void* q, int32_t q_dtype, const void* k, const void
     }
     return hip_rc(bt::launch_prefill8(p, head_dim, (hipStream_t)stream));
   }
-  return hip_rc(bt::launch_prefill(p, head_dim, (hipStream_t)stream));
+  return BT_ENOTSUP;
 }
 
 int bt_gqa_prefill(const void* q, int32_t q_dtype, const void* k, const void* v, int64_t q_stride_tok,

@@ -1,19 +1,28 @@
 // Causal GQA prefill on CDNA4 fp16 MFMA with two waves per SIMD.
 //
-// Same contract as gqa_prefill.hip (the causal SDPA of prefill.py:56-68 and
-// the banded chunked prefill of qwen36_moe.py:394-428: query row i at
-// absolute position q_offset + i attends keys 0 .. q_offset + i), with a
+// Computes, for every new query row i (absolute position p0 + i, where p0 =
+// q_offset tokens are already in the cache) and every query head h (kv head
+// h / group),
+//     out[i, h] = softmax_{j <= p0+i} (q_i . k_j * scale) . V_j
+// over the p0 + S keys of the cache -- the F.scaled_dot_product_attention
+// (is_causal=True, enable_gqa=True) call of _prefill_attn (breezetoken/model/
+// prefill.py:56-68, p0 = 0) and the banded-mask chunked prefill of
+// Qwen36MoE._attn_batch (breezetoken/model/qwen36_moe.py:394-428) -- with a
 // work decomposition that keeps two waves resident on every SIMD:
 //  * a work-group of 8 waves shares one K tile and one V^T tile in LDS; wave w
-//    owns query head (w % G) of the kv group and 16 query positions
-//    [q0 + (w / G) * 16, +16), G in {1, 2, 4, 8};
+//    owns query head (w % G) of a subset of G heads of the kv group and 16
+//    query positions [q0 + (w / G) * 16, +16), G in {1, 2, 4, 8}: the largest
+//    power of two that divides the group size (so a group of 6 runs as 3
+//    subsets of 2 heads, each subset's work-groups reading the same K/V);
 //  * per 64-key block a wave runs 32 v_mfma_f32_16x16x32_f16 for S^T = K.Q^T
 //    (K from LDS, Q^T in registers) and 32 for O^T += V^T.P^T (V^T from LDS,
 //    P^T built in registers from the S^T accumulators).  Per wave that is 64
-//    accumulators of O, 32 registers of Q and 16 of S -- half of the
-//    one-wave-per-SIMD layout -- so two waves fit in the register file and
-//    hide each other's LDS, copy and barrier waits;
-//  * q (f32 or bf16) enters as fp16 with a power-of-two scale per query row,
+//    accumulators of O, 32 registers of Q and 16 of S (64 of Q for f32 q,
+//    below), so two waves fit in the register file and hide each other's
+//    LDS, copy and barrier waits;
+//  * q enters as fp16 with a power-of-two scale per query row: bf16 q
+//    converts exactly, f32 q as two fp16 terms (hi + lo, two MFMAs per K
+//    fragment) so the scores keep f32 q's precision at any magnitude;
 //    K and V come from the pre-pass's fp16 images (gqa_prefill_vt.hip), each
 //    scaled per 64-key block; the softmax takes all three factors back
 //    exactly in its exp2 argument;
@@ -28,7 +37,7 @@
 //  * the online softmax (log2 domain, lazy rescaling by 2^8) of block kb runs
 //    beside the P.V product of block kb - 1; tiles are double-buffered with
 //    two barriers per block and every copy issued as soon as its buffer is
-//    free, as in the one-wave kernel;
+//    free;
 //  * a work-group runs one or two segments (key-block ranges of a query
 //    block): the whole query block, a chunk of it under the uniform split, or
 //    its share of a query-block pair under the paired split (see
@@ -51,6 +60,10 @@ typedef float float2v_8 __attribute__((ext_vector_type(2)));
 template <int B>
 struct Buf8 {
   static constexpr int value = B;
+};
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
 };
 
 constexpr int kKB8 = kPrefillKeyBlock;  // keys per block (64)
@@ -101,7 +114,9 @@ __host__ __device__ inline int pair_chunks(int qb, int nqb, int parts, NB n_bloc
 // pre-pass launch.
 // PAIRED: the paired split (two segments per work-group at most); its own
 // instantiation, so the single-segment kernel keeps one copy of the loop.
-template <int D, bool DIRECT, bool PAIRED>
+// LO: f32 q as two fp16 terms (hi + lo, see split_f16x2), each K fragment
+// feeding one MFMA per term, so the scores match f32 q at any magnitude.
+template <int D, bool DIRECT, bool PAIRED, bool LO>
 __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillParams p) {
   constexpr int kDSteps = D / 32;      // K-dimension steps of Q.K^T (32 per MFMA)
   constexpr int kDTiles = D / 16;      // 16-row d tiles of O^T
@@ -126,8 +141,10 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int kvh = blockIdx.y;
-  const int G = p.group;                    // 1, 2, 4 or 8 (checked by the launcher)
+  const int ysub = blockIdx.y;              // (kv head, head subset)
+  const int kvh = ysub / p.head_subs;
+  const int G = p.sub_group;                // 1, 2, 4 or 8 (checked by the launcher)
+  const int head_base = kvh * p.group + (ysub % p.head_subs) * G;
   const int pos_per_wg = kQ8 * (kWaves8 / G);
   const int S = p.seqlen;
   const int P0 = p.q_offset;
@@ -140,7 +157,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     const int wg_q0 = qblk * pos_per_wg;
     const int q0 = wg_q0 + (wave / G) * kQ8;
     const int last = kb1 - 1;
-    const int head = kvh * G + wave % G;
+    const int head = head_base + wave % G;
 
     const size_t head_img = (size_t)kvh * p.img_blocks * kKB8 * D;  // this kv head's images
     const __amdgpu_buffer_rsrc_t krs = rsrc8(p.kimg + head_img, (uint32_t)nblk * kImg);
@@ -203,7 +220,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
         eb = sload(vexp, b);
       }
     };
-    // Copy schedule (as in the one-wave kernel):
+    // Copy schedule:
     //   start of step kb: V_kb -> V buffer kb % 2; after the mid barrier: K_{kb+2}
     //   -> K buffer kb % 2; the mid barrier publishes V_{kb-1}, the end barrier
     //   K_{kb+1}.  No copy goes past the last block (a short work-group would
@@ -254,13 +271,15 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     int ek_c, eb_c;
     if constexpr (!DIRECT) scales(kb0, ek_c, eb_c);
     u32x4 qop[kDSteps];
+    u32x4 qlo[LO ? kDSteps : 1];
     float c_col;
     {
       const int qrow = min(q0 + i16, S - 1);
       const int64_t off = (int64_t)qrow * p.q_stride_tok + (int64_t)head * p.q_stride_head + g4 * 8;
-      const int eq = q_row_f16(p.q, p.q_f32 != 0, off, 32, qop, [](uint32_t mx) {
-        return xor_umax<32>(xor_umax<16>(mx));  // the row's four lane groups
-      });
+      auto reduce = [](uint32_t mx) { return xor_umax<32>(xor_umax<16>(mx)); };  // the row's four lane groups
+      int eq;
+      if constexpr (LO) eq = q_row_f16_lo(reinterpret_cast<const float*>(p.q), off, 32, qop, qlo, reduce);
+      else eq = q_row_f16(p.q, p.q_f32 != 0, off, 32, qop, reduce);
       c_col = __builtin_ldexpf(p.scale_log2, eq);
     }
     if constexpr (DIRECT) {
@@ -359,6 +378,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
           const u32x4 a = *reinterpret_cast<const u32x4*>(kb_ + (sub * 16 + i16) * (D * 2) +
                                                             (((st * 4 + g4) ^ i16) * 16));
           sacc[sub] = mfma16_f16(a, qop[st], st == 0 ? zero : sacc[sub]);
+          if constexpr (LO) sacc[sub] = mfma16_f16(a, qlo[st], sacc[sub]);
         }
       }
     };
@@ -497,7 +517,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     if (nchunks > 1) {
       // One chunk of a split query block: normalised partial and LSE of row
       // (wave, query column) for prefill_combine_kernel.
-      const int64_t slot = ((int64_t)kvh * nqb + qblk) * p.max_chunks + chunk;
+      const int64_t slot = ((int64_t)ysub * nqb + qblk) * p.max_chunks + chunk;
       const int row = wave * kQ8 + i16;
       float* prow = p.part + (slot * kRows8 + row) * D;
       const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
@@ -573,18 +593,18 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
   constexpr int kD4 = D / 4;
   constexpr int kRowsPerGroup = 256 / kD4;  // rows whose items one work-group merges
   constexpr int kBatch = 8;                 // chunks whose loads are in flight together
-  const int G = p.group;
+  const int G = p.sub_group;
   const int pos_per_wg = kQ8 * (kWaves8 / G);
   const int S = p.seqlen;
   const int nqb = (S + pos_per_wg - 1) / pos_per_wg;
   const int qblk = nqb - 1 - (int)blockIdx.x;
-  const int kvh = blockIdx.y;
+  const int ysub = blockIdx.y;  // (kv head, head subset), as in the main kernel
   const int wg_q0 = qblk * pos_per_wg;
   auto n_blocks = [&](int qb) { return (p.q_offset + min(S, (qb + 1) * pos_per_wg) + kKB8 - 1) / kKB8; };
   const int nchunks = p.pair_parts > 0 ? pair_chunks(qblk, nqb, p.pair_parts, n_blocks)
                                        : (n_blocks(qblk) + p.kb_chunk - 1) / p.kb_chunk;
   if (nchunks <= 1) return;
-  const int64_t slot0 = ((int64_t)kvh * nqb + qblk) * p.max_chunks;
+  const int64_t slot0 = ((int64_t)ysub * nqb + qblk) * p.max_chunks;
   const int t = threadIdx.x;
   const int row = (int)blockIdx.z * kRowsPerGroup + t / kD4;
   const int d = (t % kD4) * 4;
@@ -629,7 +649,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
   }
   const float inv = sum > 0.f ? 1.f / sum : 0.f;
   acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
-  const int head = kvh * G + w % G;
+  const int head = (ysub / p.head_subs) * p.group + (ysub % p.head_subs) * G + w % G;
   const int64_t orow = (int64_t)q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
   if (p.out_bf16) {
     const u32x2 pk2 = {pack2(f32_to_bf16_bits(acc.x), f32_to_bf16_bits(acc.y)),
@@ -704,39 +724,47 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
 }
 
 bool prefill8_serves(int group, int head_dim) {
-  return (group == 1 || group == 2 || group == 4 || group == 8) && (head_dim == 128 || head_dim == 256);
+  return group >= 1 && group <= 8 && (head_dim == 128 || head_dim == 256);
 }
 
+int prefill8_sub_group(int group) { return group & -group; }  // largest power of two dividing it
+
 hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t stream) {
-  const int pos_per_wg = kQ8 * (kWaves8 / p.group);
+  if (p.sub_group < 1 || p.head_subs < 1 || p.sub_group * p.head_subs != p.group || kWaves8 % p.sub_group)
+    return hipErrorInvalidValue;
+  const int pos_per_wg = kQ8 * (kWaves8 / p.sub_group);
   const int nqb = (p.seqlen + pos_per_wg - 1) / pos_per_wg;
   const bool paired = p.pair_parts > 0;
   const bool split = p.kb_chunk > 0 || (paired && p.max_chunks > 1);  // partials and the combine
   if (paired && p.kb_chunk > 0) return hipErrorInvalidValue;
   if (split && (p.max_chunks < 1 || p.max_chunks > kMaxChunks || !p.part || !p.lse)) return hipErrorInvalidValue;
-  const dim3 grid = paired ? dim3(((nqb + 1) / 2) * p.pair_parts, p.kv_heads, 1)
-                           : dim3(nqb, p.kv_heads, p.kb_chunk > 0 ? p.max_chunks : 1);
-  const dim3 cgrid(nqb, p.kv_heads, kRows8 * head_dim / 4 / 256);
+  const int ys = p.kv_heads * p.head_subs;  // grid y: (kv head, head subset)
+  const dim3 grid = paired ? dim3(((nqb + 1) / 2) * p.pair_parts, ys, 1)
+                           : dim3(nqb, ys, p.kb_chunk > 0 ? p.max_chunks : 1);
+  const dim3 cgrid(nqb, ys, kRows8 * head_dim / 4 / 256);
   // Work-groups with at most two key blocks each convert them themselves,
   // unless the caller keeps the images for later chunks.
   const int longest = (p.q_offset + p.seqlen + kKB8 - 1) / kKB8;
   const bool direct = !p.keep_images && !paired && (p.kb_chunk > 0 ? p.kb_chunk : longest) <= 2;
   if (!direct) {
-    const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder16, stream);
+    const hipError_t vt_rc = launch_prefill_vts(p, head_dim, stream);
     if (vt_rc != hipSuccess) return vt_rc;
   }
+  auto launch = [&](auto dsel, auto losel) {
+    constexpr int Dk = decltype(dsel)::value;
+    constexpr bool LOk = decltype(losel)::value;
+    if (paired) hipLaunchKernelGGL((gqa_prefill8_kernel<Dk, false, true, LOk>), grid, dim3(kWaves8 * 64), 0, stream, p);
+    else if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<Dk, true, false, LOk>), grid, dim3(kWaves8 * 64), 0, stream, p);
+    else hipLaunchKernelGGL((gqa_prefill8_kernel<Dk, false, false, LOk>), grid, dim3(kWaves8 * 64), 0, stream, p);
+    if (split) hipLaunchKernelGGL(prefill_combine_kernel<Dk>, cgrid, dim3(256), 0, stream, p);
+  };
+  // f32 q takes the two-term (hi + lo) Q.K^T; bf16 q converts to fp16 exactly.
   switch (head_dim) {
     case 128:
-      if (paired) hipLaunchKernelGGL((gqa_prefill8_kernel<128, false, true>), grid, dim3(kWaves8 * 64), 0, stream, p);
-      else if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<128, true, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
-      else hipLaunchKernelGGL((gqa_prefill8_kernel<128, false, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
-      if (split) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
+      if (p.q_f32) launch(Buf8<128>{}, BoolC<true>{}); else launch(Buf8<128>{}, BoolC<false>{});
       break;
     case 256:
-      if (paired) hipLaunchKernelGGL((gqa_prefill8_kernel<256, false, true>), grid, dim3(kWaves8 * 64), 0, stream, p);
-      else if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<256, true, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
-      else hipLaunchKernelGGL((gqa_prefill8_kernel<256, false, false>), grid, dim3(kWaves8 * 64), 0, stream, p);
-      if (split) hipLaunchKernelGGL(prefill_combine_kernel<256>, cgrid, dim3(256), 0, stream, p);
+      if (p.q_f32) launch(Buf8<256>{}, BoolC<true>{}); else launch(Buf8<256>{}, BoolC<false>{});
       break;
     default: return hipErrorInvalidValue;
   }

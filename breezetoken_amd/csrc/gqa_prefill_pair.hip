@@ -75,9 +75,9 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 struct PairShape {
   int nqt, hg, pos, nsub;
 };
-__host__ __device__ inline PairShape pair_shape(int group) {
+__host__ __device__ inline PairShape pair_shape(int group, int nqt) {
   PairShape s;
-  s.nqt = 2;
+  s.nqt = nqt;
   s.hg = group < 4 * s.nqt ? group : 4 * s.nqt;
   s.pos = 16 * 4 * s.nqt / s.hg;
   s.nsub = group / s.hg;
@@ -94,10 +94,11 @@ struct Sel {
   static constexpr bool value = B;
 };
 
-template <int D, int GRP, typename XB>
+// NQT q-tiles per wave; LO: f32 q as two fp16 terms (hi + lo, see
+// split_f16x2), each K fragment feeding one MFMA per term.
+template <int D, int NQT, bool LO, int GRP, typename XB>
 __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char* K0, unsigned char* K1,
                                            unsigned char* V0, unsigned char* V1, XB xbuf, float* xs) {
-  constexpr int NQT = 2;
   constexpr int kDSteps = D / 32;
   constexpr int kDTiles = D / 16;
   constexpr int kRowBytes = D * 2;
@@ -109,7 +110,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   const int gw = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) & 3);
   const int i16 = lane & 15;
   const int g4 = lane >> 4;
-  const PairShape sh = pair_shape(p.group);
+  const PairShape sh = pair_shape(p.group, NQT);
   const int kvh = (int)blockIdx.y / sh.nsub;
   const int sub = (int)blockIdx.y % sh.nsub;
   const int S = p.seqlen;
@@ -187,6 +188,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // c_col = scale * log2(e) * 2^eq restores it in the exp2 argument.  Rows
   // past the prompt read the last row (their output is not stored).
   u32x4 qop[NQT][kDSteps];
+  u32x4 qlo[LO ? NQT : 1][kDSteps];
   float c_col[NQT];
   // One pass over q: every load of the block is issued before any is used (the
   // raw values take the registers O frees between blocks), then each row's
@@ -204,7 +206,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       const int row = min(blk * sh.pos + poff[t] + i16, S - 1);
       off[t] = (int64_t)row * p.q_stride_tok + (int64_t)head[t] * p.q_stride_head + g4 * 8;
     }
-    if (p.q_f32) {
+    if constexpr (LO) {
       const float* qf = reinterpret_cast<const float*>(p.q);
       float4 raw[NQT][kDSteps][2];
 #pragma unroll
@@ -216,24 +218,20 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
         }
 #pragma unroll
       for (int t = 0; t < NQT; ++t) {
-        uint32_t mx = 0;
-#pragma unroll
-        for (int st = 0; st < kDSteps; ++st)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float4 v = raw[t][st][h];
-            mx = max(mx, max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
-                             max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu)));
-          }
-        const int eq = row_scale(t, mx);
+        const int eq = row_scale(t, absmax_bits(raw[t]));
 #pragma unroll
         for (int st = 0; st < kDSteps; ++st) {
           const float4 a = raw[t][st][0], b = raw[t][st][1];
-          qop[t][st] = u32x4{pack_f16x2_scaled(a.x, a.y, eq), pack_f16x2_scaled(a.z, a.w, eq),
-                             pack_f16x2_scaled(b.x, b.y, eq), pack_f16x2_scaled(b.z, b.w, eq)};
+          uint32_t h[4], l[4];
+          split_f16x2(a.x, a.y, eq, h[0], l[0]);
+          split_f16x2(a.z, a.w, eq, h[1], l[1]);
+          split_f16x2(b.x, b.y, eq, h[2], l[2]);
+          split_f16x2(b.z, b.w, eq, h[3], l[3]);
+          qop[t][st] = u32x4{h[0], h[1], h[2], h[3]};
+          qlo[t][st] = u32x4{l[0], l[1], l[2], l[3]};
         }
       }
-    } else {
+    } else {  // bf16 q (the launcher sends f32 q to the LO instantiation)
 #pragma unroll
       for (int t = 0; t < NQT; ++t)
 #pragma unroll
@@ -318,7 +316,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // the step's scale exponents in the *_d scalars.
   constexpr int kNow = 1;
   u32x4 pk[NQT];
-  float xd[NQT - kNow][8];
+  float xd[NQT > kNow ? NQT - kNow : 1][8];
   int shift_d = 0, ek_d = 0, eold_d = 0, enew_d = 0;
   // Block scales (V^T and K exponents) of a step's unit, read one step ahead
   // into scalar registers so the softmax never waits for them.  Steps past this
@@ -389,6 +387,13 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       for (int t = 0; t < NQT; ++t) {
         sacc[0][t] = mfma_f16(a0, qop[t][st], sacc[0][t]);
         sacc[1][t] = mfma_f16(a1, qop[t][st], sacc[1][t]);
+      }
+      if constexpr (LO) {
+#pragma unroll
+        for (int t = 0; t < NQT; ++t) {
+          sacc[0][t] = mfma_f16(a0, qlo[t][st], sacc[0][t]);
+          sacc[1][t] = mfma_f16(a1, qlo[t][st], sacc[1][t]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -626,10 +631,9 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
 
 }  // namespace
 
-template <int D>
+template <int D, int NQT, bool LO>
 __global__ __launch_bounds__(2 * kGWaves * 64, 1) void gqa_prefill_pair_kernel(PrefillParams p) {
   constexpr int kTile = kUnit * D * 2;
-  constexpr int NQT = 2;
   // Eight tile buffers (two per group per stage); after the key loop group A
   // hands its partial to group B through the first ones.
   __shared__ __attribute__((aligned(1024))) unsigned char kA0[kTile], kA1[kTile], vA0[kTile], vA1[kTile];
@@ -651,8 +655,8 @@ __global__ __launch_bounds__(2 * kGWaves * 64, 1) void gqa_prefill_pair_kernel(P
     return reinterpret_cast<float*>(b);
   };
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  if (wave < kGWaves) pair_group<D, 0>(p, kA0, kA1, vA0, vA1, xbuf, xs);
-  else pair_group<D, 1>(p, kB0, kB1, vB0, vB1, xbuf, xs);
+  if (wave < kGWaves) pair_group<D, NQT, LO, 0>(p, kA0, kA1, vA0, vA1, xbuf, xs);
+  else pair_group<D, NQT, LO, 1>(p, kB0, kB1, vB0, vB1, xbuf, xs);
 }
 
 bool prefill_pair_serves(int group, int head_dim) {
@@ -660,24 +664,32 @@ bool prefill_pair_serves(int group, int head_dim) {
   return group == 1 || group == 2 || group == 4 || group == 8;
 }
 
+// Work-groups of the bf16-q launch (two q-tiles per wave); the f32-q launch
+// (one q-tile per wave, hi + lo q) has twice as many, each with half the work.
 int prefill_pair_grid(int seqlen, int group, int kv_heads) {
-  const PairShape sh = pair_shape(group);
+  const PairShape sh = pair_shape(group, 2);
   const int nqb = (seqlen + sh.pos - 1) / sh.pos;
   return ((nqb + 1) / 2) * kv_heads * sh.nsub;
 }
 
 hipError_t launch_prefill_pair(const PrefillParams& p, int head_dim, hipStream_t stream) {
-  const PairShape sh = pair_shape(p.group);
+  // bf16 q converts to fp16 exactly: two q-tiles per wave.  f32 q takes two
+  // fp16 terms, whose registers leave room for one q-tile per wave.
+  const int nqt = p.q_f32 ? 1 : 2;
+  const PairShape sh = pair_shape(p.group, nqt);
   const int nqb = (p.seqlen + sh.pos - 1) / sh.pos;
   const dim3 grid((nqb + 1) / 2, p.kv_heads * sh.nsub);
-  const hipError_t vt_rc = launch_prefill_vts(p, head_dim, kVtOrder16, stream);
+  const hipError_t vt_rc = launch_prefill_vts(p, head_dim, stream);
   if (vt_rc != hipSuccess) return vt_rc;
+  const dim3 block(2 * kGWaves * 64);
   switch (head_dim) {
     case 128:
-      hipLaunchKernelGGL(gqa_prefill_pair_kernel<128>, grid, dim3(2 * kGWaves * 64), 0, stream, p);
+      if (p.q_f32) hipLaunchKernelGGL((gqa_prefill_pair_kernel<128, 1, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((gqa_prefill_pair_kernel<128, 2, false>), grid, block, 0, stream, p);
       break;
     case 256:
-      hipLaunchKernelGGL(gqa_prefill_pair_kernel<256>, grid, dim3(2 * kGWaves * 64), 0, stream, p);
+      if (p.q_f32) hipLaunchKernelGGL((gqa_prefill_pair_kernel<256, 1, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((gqa_prefill_pair_kernel<256, 2, false>), grid, block, 0, stream, p);
       break;
     default: return hipErrorInvalidValue;
   }

@@ -9,13 +9,9 @@
 // significant bits).  e goes to vexp[g * nblk + b]; the attention kernels fold
 // it into P (see vexp_next in bt_common.h).  Layout: block b of head g at vt +
 // (g * nblk + b) * 64 * D as 8 key chunks; chunk c holds at row d the 8
-// values V[b*64 + key][d] (16 bytes) of
-//   order kVtOrder16: key = (c/4)*32 + (c%4)*4 + {0, 1, 2, 3, 16, 17, 18, 19},
-//     the order in which lane group c%4 of a 16x16 MFMA result holds P of the
-//     32-key half c/4;
-//   order kVtOrder32: key = (c/2)*16 + (c%2)*4 + {0, 1, 2, 3, 8, 9, 10, 11},
-//     the order in which a 32x32 MFMA result's registers hold P of the 16-key
-//     step c/2 for lane half c%2.
+// values V[b*64 + key][d] (16 bytes) of key = (c/4)*32 + (c%4)*4 + {0, 1, 2,
+// 3, 16, 17, 18, 19}: the order in which lane group c%4 of a 16x16 MFMA
+// result holds P of the 32-key half c/4.
 // Grid z = 0 converts K, z = 1 V (two work-groups per block, so a CU holds
 // one's loads in flight while the other converts and stores).  For V, one
 // thread per (chunk, 8-column slice) transposes an 8 x 8 tile in registers; the block's image is assembled in LDS and stored linearly (1 KiB
@@ -46,7 +42,7 @@ namespace {
 typedef _Float16 half2_v __attribute__((ext_vector_type(2)));
 typedef float float2_v __attribute__((ext_vector_type(2)));
 
-template <int D, int ORDER>
+template <int D>
 __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
   constexpr int kDC = D / 8;                 // 16-byte column chunks per row
   constexpr int kItems = 8 * kDC;            // (chunk, column chunk) items per block
@@ -117,8 +113,7 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
   if (item < kItems) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int key = ORDER == kVtOrder16 ? blk * kBlk + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16
-                                          : blk * kBlk + (c >> 1) * 16 + (c & 1) * 4 + (j & 3) + (j >> 2) * 8;
+      const int key = blk * kBlk + (c >> 2) * 32 + (c & 3) * 4 + (j & 3) + (j >> 2) * 16;
       rows[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((uint32_t)key * row_bytes + (uint32_t)dc * 16), 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) mx = max(mx, max(rows[j][i] & 0x7fffu, (rows[j][i] >> 16) & 0x7fffu));
@@ -158,21 +153,14 @@ __global__ __launch_bounds__(256) void prefill_vts_kernel(PrefillParams p) {
 
 }  // namespace
 
-hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, int order, hipStream_t stream) {
+hipError_t launch_prefill_vts(const PrefillParams& p, int head_dim, hipStream_t stream) {
   const int nblk = (p.q_offset + p.seqlen + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
-  if (order != kVtOrder16 && order != kVtOrder32) return hipErrorInvalidValue;
   if (p.img_blocks < nblk || p.img_first < 0 || p.img_first > nblk) return hipErrorInvalidValue;
   if (p.img_first == nblk) return hipSuccess;  // every block is already in the images
   const dim3 grid((nblk - p.img_first) * p.kv_heads, 1, 2);
   switch (head_dim) {
-    case 128:
-      if (order == kVtOrder16) hipLaunchKernelGGL((prefill_vts_kernel<128, kVtOrder16>), grid, dim3(256), 0, stream, p);
-      else hipLaunchKernelGGL((prefill_vts_kernel<128, kVtOrder32>), grid, dim3(256), 0, stream, p);
-      break;
-    case 256:
-      if (order == kVtOrder16) hipLaunchKernelGGL((prefill_vts_kernel<256, kVtOrder16>), grid, dim3(256), 0, stream, p);
-      else hipLaunchKernelGGL((prefill_vts_kernel<256, kVtOrder32>), grid, dim3(256), 0, stream, p);
-      break;
+    case 128: hipLaunchKernelGGL((prefill_vts_kernel<128>), grid, dim3(256), 0, stream, p); break;
+    case 256: hipLaunchKernelGGL((prefill_vts_kernel<256>), grid, dim3(256), 0, stream, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -277,3 +277,26 @@ def test_head_major_cache_decode(hip_backend, seq):
     assert_close(out, ref)
     pos = torch.tensor([seq - 1], dtype=torch.int32, device="cuda")
     assert_close(hip_backend.attention_fixed(qd, kd.transpose(0, 1), vd.transpose(0, 1), pos, scale), ref)
+
+
+@pytest.mark.parametrize("heads,ctx,std", [(8, 4096, 4), (8, 4096, 8), (8, 4096, 16), (8, 32768, 16),
+                                           (16, 8192, 16), (8, 300, 32)])
+def test_f32_q_score_scales(hip_backend, heads, ctx, std):
+    """Scores of the scale q/k RMSNorm weights of 2-3 produce (standard
+    deviation 4-16, and 32): q (f32) and K both scaled by sqrt(std).  The split
+    kernel takes q as bf16 hi + lo (~16 significant bits) after folding in
+    scale * log2(e), and P as bf16 hi + lo, so the error stays far below the
+    gate; checked for the fixed-capacity call at the device position."""
+    g = torch.Generator().manual_seed(heads * 7 + ctx + std)
+    a = std**0.5
+    q = torch.randn(heads, 256, generator=g) * a
+    cap = ctx + 64
+    k = (torch.randn(cap, 2, 256, generator=g) * a).to(torch.bfloat16)
+    v = torch.randn(cap, 2, 256, generator=g).to(torch.bfloat16)
+    pos = torch.tensor([ctx - 1], dtype=torch.int32, device="cuda")
+    print(f"[decode f32 q] H={heads} ctx={ctx} score std {std}", flush=True)
+    out = hip_backend.attention_fixed(q.cuda(), k.cuda(), v.cuda(), pos, 256**-0.5)
+    ref = orc.torch_attention(q, k[:ctx].float(), v[:ctx].float(), 256**-0.5)
+    err, cos = orc.compare(out.cpu().numpy(), ref.numpy())
+    print(f"    max-abs {err:.3e} cosine {cos:.9f}", flush=True)
+    assert err <= ATOL and cos >= COS

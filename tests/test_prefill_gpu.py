@@ -66,9 +66,13 @@ def test_c4_prefill_8192_sampled_rows(hip_backend):
         _close(out[i], ref)
 
 
-@pytest.mark.parametrize("steps", [128, 2048])
+@pytest.mark.parametrize("steps", [128, 512, 2048, 8192])
 def test_c4_prefill_bf16_output(hip_backend, steps):
+    """Config 4's output format (bf16), on every path the benchmark times: the
+    direct-tile kernel (S = 128), the split-key schedule (512, 2048) and the
+    pair kernel (8192)."""
     q, k, v, scale = wl.c4_inputs(steps)
+    print(f"[c4 bf16 out] S={steps}", flush=True)
     ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
     out = hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale, out_dtype=torch.bfloat16)
     assert out.dtype == torch.bfloat16
@@ -89,8 +93,8 @@ def test_ragged_prompt_lengths(hip_backend, steps):
                                           (16, 2, 128), (4, 2, 128),
                                           (6, 2, 256), (12, 2, 128), (10, 2, 256), (3, 1, 128)])
 def test_other_group_sizes(hip_backend, heads, kv, dim):
-    """Group sizes 1, 2, 4, 8 at D = 128 / 256 run the two-waves-per-SIMD kernel;
-    3, 5, 6 take the one-wave-per-SIMD kernel."""
+    """Group sizes 1, 2, 4, 8 at D = 128 / 256 run the two-waves-per-SIMD kernel
+    directly; 3, 5, 6 run it as subsets of 1 or 2 heads."""
     q, k, v, scale = _inputs(300, heads, kv, dim, seed=heads * 100 + kv)
     ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
     _close(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale), ref)
@@ -152,7 +156,7 @@ def test_chunked_prefill_query_offset(hip_backend, steps, pos0):
 @pytest.mark.parametrize("heads,kv,dim,steps,pos0", [(8, 2, 256, 100, 37), (4, 4, 256, 70, 129), (8, 4, 128, 200, 64),
                                                      (6, 2, 256, 90, 300)])
 def test_chunked_prefill_other_group_sizes(hip_backend, heads, kv, dim, steps, pos0):
-    """Query offsets for group sizes 4, 1, 2 (two-waves-per-SIMD kernel) and 3 (one-wave kernel)."""
+    """Query offsets for group sizes 4, 1, 2 and 3 (three single-head subsets)."""
     g = torch.Generator().manual_seed(heads * 1000 + kv * 100 + pos0)
     q = torch.randn(steps, heads, dim, generator=g).to(torch.bfloat16)
     k = torch.randn(pos0 + steps, kv, dim, generator=g).to(torch.bfloat16)
@@ -320,11 +324,6 @@ def test_short_prompt_direct_tiles_equal_images(hip_backend, steps, q_offset, he
     q = torch.randn(steps, heads, dim, generator=g)
     k = torch.randn(total, kv, dim, generator=g)
     v = torch.randn(total, kv, dim, generator=g)
-    if pattern != "normal":
-        # bf16-valued q converts to fp16 exactly; with f32 q, its fp16 rounding
-        # error grows with the score scale (K up to 4x unit magnitude here) and
-        # would reach the gate by itself (unit-magnitude K: the normal pattern)
-        q = q.to(torch.bfloat16).float()
     if pattern == "large_v_tiny_k":
         v, k = v * 3e4, k * 1e-3
     elif pattern == "blockwise":  # a different magnitude in every 64-key block
@@ -416,12 +415,42 @@ def test_pair_kernel_shapes(hip_backend, steps, heads, kv, dim, q_offset, q_f32)
     _close(out, ref)
 
 
-@pytest.mark.parametrize("steps,heads,kv,dim", [(2048, 6, 2, 256), (1500, 10, 2, 128), (4096, 14, 2, 128),
-                                                (3001, 12, 2, 256)])
-def test_one_wave_kernel_long_prompts(hip_backend, steps, heads, kv, dim):
-    """Group sizes 3, 5, 6, 7 (the one-wave-per-SIMD kernel) on long prompts:
-    every row against the oracle."""
+@pytest.mark.parametrize("steps,heads,kv,dim,q_f32", [(2048, 6, 2, 256, False), (1500, 10, 2, 128, True),
+                                                      (4096, 14, 2, 128, False), (3001, 12, 2, 256, True)])
+def test_head_subset_group_sizes_long_prompts(hip_backend, steps, heads, kv, dim, q_f32):
+    """Group sizes 3, 5, 6, 7 (subsets of 1 or 2 heads, each with its own
+    split plan) on long prompts: every row against the oracle."""
     q, k, v, scale = _inputs(steps, heads, kv, dim, seed=steps + heads)
-    print(f"[one-wave] S={steps} H={heads} Hkv={kv} D={dim}", flush=True)
+    if q_f32:
+        q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(steps))
+    print(f"[head subsets] S={steps} H={heads} Hkv={kv} D={dim} f32q={q_f32}", flush=True)
     ref = orc.torch_prefill_attention(q.float(), k.float(), v.float(), scale)
     _close(hip_backend.attention_prefill(q.cuda(), k.cuda(), v.cuda(), scale), ref)
+
+
+@pytest.mark.parametrize("q_f32", [False, True])
+def test_kept_images_chunk_on_the_pair_kernel(hip_backend, q_f32):
+    """A chunk long enough for the pair kernel (4,096 queries at G = 8) behind a
+    1,000-key prefix, through images laid out for an 8,192-slot cache (more
+    blocks than the call's keys, conversion from block 15 on): equal bit for
+    bit to the call that builds fresh images, and to the banded oracle."""
+    cap, heads, kv, dim = 8192, 16, 2, 256
+    chunks = [(0, 1000), (1000, 4096)]
+    assert _pair_grid(4096, heads, kv) >= hip_backend.num_cus
+    g = torch.Generator().manual_seed(8192 + q_f32)
+    k = torch.randn(cap, kv, dim, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(cap, kv, dim, generator=g).to(torch.bfloat16).cuda()
+    q_all = torch.randn(5096, heads, dim, generator=g)
+    q_all = (q_all if q_f32 else q_all.to(torch.bfloat16)).cuda()
+    scale = dim**-0.5
+    images = hip_backend.prefill_images(cap, kv, dim)
+    for pos0, s in chunks:
+        print(f"[kept images] chunk {pos0}+{s} f32q={q_f32}", flush=True)
+        q = q_all[pos0 : pos0 + s]
+        kk, vv = k[: pos0 + s], v[: pos0 + s]
+        got = hip_backend.attention_prefill(q, kk, vv, scale, q_offset=pos0, images=images)
+        want = hip_backend.attention_prefill(q, kk, vv, scale, q_offset=pos0)
+        assert torch.equal(got, want), (pos0, s)
+        assert images.valid_keys == pos0 + s
+    ref = orc.torch_prefill_banded(q.float().cpu(), kk.float().cpu(), vv.float().cpu(), pos0, scale)
+    _close(got, ref)
