@@ -146,10 +146,12 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvParams p) {
 hipError_t launch_gemv(const GemvParams& p, int vec, hipStream_t stream) {
   const int tile = 64 * vec;
   const dim3 grid((p.N + tile - 1) / tile, p.splits);
-  // A share of 61..64 rows is one batch of 16 rows per wave (two batches of 8
-  // otherwise); shorter shares keep 8, so no wave walks them one row at a time.
+  // A share of exactly 64 rows is one batch of 16 rows per wave (two batches
+  // of 8 otherwise).  Other shares keep 8: in a share of 61..63 rows some
+  // waves hold 15, miss the 16-row batch and would load them one at a time
+  // while the work-group waits for them at the reduction.
   const int k_per = (p.K + p.splits - 1) / p.splits;
-  const bool one_pass = k_per > kGemvWaves * 15 && k_per <= kGemvWaves * 16;
+  const bool one_pass = k_per == kGemvWaves * 16;
   if (vec == 8 && one_pass) hipLaunchKernelGGL((gemv_bf16_kernel<8, 16>), grid, dim3(256), 0, stream, p);
   else if (vec == 8) hipLaunchKernelGGL((gemv_bf16_kernel<8, 8>), grid, dim3(256), 0, stream, p);
   else if (vec == 4 && one_pass) hipLaunchKernelGGL((gemv_bf16_kernel<4, 16>), grid, dim3(256), 0, stream, p);

@@ -27,7 +27,7 @@ from __future__ import annotations
 
 import torch
 
-SLOT_ALIGN = 32  # tokens per decode tile
+SLOT_ALIGN = 32  # the reference's K/V tile (cap % block_n == 0, attention.py:227-228): two 16-token decode tiles
 
 
 def padded_slots(capacity: int) -> int:

@@ -102,13 +102,12 @@ int bt_gqa_decode(const void* q, int32_t q_dtype, int64_t q_stride_seq, const vo
 
 /* bt_gqa_decode without a caller workspace, for callers that cannot allocate
  * (code under hipGraph capture that must not call hipMalloc, tight serving
- * loops, harnesses that forbid allocation).  No counterpart in the reference,
- * whose launch wrappers allocate Lse/Part per call (backends.py:531-533,
- * 554-556).  The split workspace is a file-scope device array of
+ * loops, harnesses that forbid allocation).  No counterpart in the reference.
+ * The split workspace is a file-scope device array of
  * BT_NOALLOC_SCRATCH_BYTES bytes, one per GPU, held from the library's load on
  * that GPU until the process ends; nothing is allocated per call.  A shape whose
  * bt_decode_workspace_bytes(heads, head_dim, batch*num_split) exceeds it returns
- * BT_ENOSPC without launching (H = 8, D = 256 fits up to 1,019 splits; the
+ * BT_ENOSPC without launching (H = 8, D = 256 fits up to 1,020 splits; the
  * configuration-2 grid uses 128).  All calls on one GPU share the array: calls
  * that overlap on one GPU (two streams, two threads) race and must be
  * serialised by the caller.  Arguments and results are those of bt_gqa_decode. */
