@@ -219,6 +219,115 @@ def prefill_mode(torch, backend, dev, calls: int, q_f32: bool = False, warmup: i
     return 0
 
 
+def floor_mode(torch, backend, dev, steps: int, warmup: int) -> int:
+    """Machine floors beside the config-2 decode kernels, in one process (the
+    probes are libbt_floor.so, built from breezetoken_amd/probes/floor.hip):
+
+    * an empty kernel as a graph node, alone in its graph and 24 in a chain;
+    * a plain streaming read of 64 MiB (config 2's K and V at 32k): 16-byte
+      non-temporal buffer loads, LPT loads per thread issued before any is
+      used, rotating over six 64 MiB buffers per graph (384 MiB, past the
+      256 MB MALL) as the decode rows rotate six layer caches, and MALL-hot
+      (one buffer six times);
+    * that read followed by a one-wave dependent kernel (the two-node shape of
+      a split + combine call);
+    * the config-2 split kernel alone and the whole call at 32k, six layer
+      caches per graph, as the headline measures them.
+    """
+    import ctypes
+
+    from breezetoken_amd import _lib
+    from breezetoken_amd import workloads as wl
+    from breezetoken_amd.kvcache import KVCache
+
+    fl = ctypes.CDLL(str(ROOT / "breezetoken_amd" / "libbt_floor.so"))
+    vp = ctypes.c_void_p
+    fl.bt_floor_empty.argtypes = [vp]
+    fl.bt_floor_read.argtypes = [vp, ctypes.c_int64, ctypes.c_int32, vp, vp]
+    fl.bt_floor_tiny.argtypes = [vp, vp, vp]
+    fl.bt_floor_read_lds.argtypes = [vp, ctypes.c_int64, vp, vp]
+    fl.bt_floor_read_rows.argtypes = [vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, vp, vp]
+    for f in (fl.bt_floor_empty, fl.bt_floor_read, fl.bt_floor_tiny, fl.bt_floor_read_lds, fl.bt_floor_read_rows):
+        f.restype = ctypes.c_int
+
+    def st():
+        return vp(torch.cuda.current_stream().cuda_stream)
+
+    def ok(rc):
+        if rc != 0:
+            raise RuntimeError(f"floor probe launch failed: {rc}")
+
+    nbytes = 64 << 20
+    res: dict = {"mode": "floor", "read_bytes": nbytes, "layers_per_graph": 6}
+    res["empty_node_us_alone"] = round(1e3 * time_graph(torch, lambda: ok(fl.bt_floor_empty(st())), steps, warmup), 3)
+    res["empty_node_us_chain24"] = round(1e3 * time_graph(
+        torch, lambda: [ok(fl.bt_floor_empty(st())) for _ in range(24)], steps, warmup) / 24, 3)
+    g = torch.Generator(device=dev).manual_seed(5)
+    bufs = [torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=dev, generator=g) for _ in range(6)]
+    out = torch.empty(nbytes // 4096, dtype=torch.int32, device=dev)
+    out2 = torch.empty(1, dtype=torch.int32, device=dev)
+    reads = {}
+    for lpt in (8, 16, 32):
+        cold = time_graph(torch, lambda: [ok(fl.bt_floor_read(b.data_ptr(), nbytes, lpt, out.data_ptr(), st()))
+                                          for b in bufs], steps, warmup) / 6
+        hot = time_graph(torch, lambda: [ok(fl.bt_floor_read(bufs[0].data_ptr(), nbytes, lpt, out.data_ptr(), st()))
+                                         for _ in bufs], steps, warmup) / 6
+        reads[lpt] = {"work_groups": nbytes // (4096 * lpt), "cold_us": round(cold * 1e3, 3),
+                      "cold_GBps": round(nbytes / (cold * 1e-3) / 1e9, 1), "mall_hot_us": round(hot * 1e3, 3)}
+    res["read_64MiB"] = reads
+    # through LDS (HBM -> LDS copies), and along token rows the way the decode
+    # kernel reads one kv head of K (two 32 MiB halves of each 64 MiB buffer:
+    # 512 of every 1,024 bytes), both cold
+    lds_us = time_graph(torch, lambda: [ok(fl.bt_floor_read_lds(b.data_ptr(), nbytes, out.data_ptr(), st()))
+                                        for b in bufs], steps, warmup) / 6
+    res["read_64MiB_via_lds"] = {"cold_us": round(lds_us * 1e3, 3),
+                                 "cold_GBps": round(nbytes / (lds_us * 1e-3) / 1e9, 1)}
+    rows = nbytes // 1024
+    for mode, key, nb_ in ((0, "read_half_rows_32MiB", nbytes // 2), (1, "read_rows_halves_adjacent_groups", nbytes),
+                           (2, "read_rows_halves_one_group", nbytes),
+                           (3, "read_rows_halves_adjacent_groups_row_loads", nbytes)):
+        us = time_graph(torch, lambda: [ok(fl.bt_floor_read_rows(b.data_ptr(), rows, 1024, mode, out.data_ptr(), st()))
+                                        for b in bufs], steps, warmup) / 6
+        res[key] = {"cold_us": round(us * 1e3, 3), "cold_GBps": round(nb_ / (us * 1e-3) / 1e9, 1)}
+    best = min(reads, key=lambda k: reads[k]["cold_us"])
+    res["read_plus_dependent_node_us"] = round(1e3 * time_graph(
+        torch, lambda: [(ok(fl.bt_floor_read(b.data_ptr(), nbytes, best, out.data_ptr(), st())),
+                         ok(fl.bt_floor_tiny(out.data_ptr(), out2.data_ptr(), st()))) for b in bufs],
+        steps, warmup) / 6, 3)
+    res["read_plus_dependent_node_lpt"] = best
+    del bufs
+    torch.cuda.empty_cache()
+    # the decode kernels, as the headline times them
+    H, HKV, D, CAP, L = 8, 2, 256, 65536, 32768
+    case = wl.c2_inputs(L, cap=CAP)
+    layers = []
+    for _ in range(6):
+        cache = KVCache(CAP, HKV, D, dev)
+        cache.k.copy_(case.k.reshape(CAP, -1))
+        cache.v.copy_(case.v.reshape(CAP, -1))
+        kv, vv = cache.views()
+        layers.append((cache, case.q.float().to(dev), kv, vv,
+                       torch.tensor([case.pos], dtype=torch.int32, device=dev)))
+    lib = _lib.lib()
+    ns = backend.pick_splits(HKV, CAP)
+    lse = torch.empty((H, ns), dtype=torch.float32, device=dev)
+    part = torch.empty((H, ns, D), dtype=torch.float32, device=dev)
+
+    def split_only():
+        for _, lq, lk, lv, lp in layers:
+            _lib.check("bt_gqa_decode_split", lib.bt_gqa_decode_split(
+                lq.data_ptr(), _lib.BT_DTYPE_F32, H * D, lk.data_ptr(), lv.data_ptr(), lk.stride(0), lk.stride(1),
+                None, lp.data_ptr(), None, CAP, 1, H, HKV, D, ns, case.scale, lse.data_ptr(), part.data_ptr(), st()))
+
+    res["c2_32k_split_us"] = round(1e3 * time_graph(torch, split_only, steps, warmup) / 6, 3)
+    res["c2_32k_call_us"] = round(1e3 * time_graph(
+        torch, lambda: [backend.attention_fixed(lq, lk, lv, lp, case.scale) for _, lq, lk, lv, lp in layers],
+        steps, warmup) / 6, 3)
+    res["c2_32k_algorithmic_bytes"] = wl.decode_bytes(L, H, HKV, D)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 CHUNKED_CASES = ((16, 128, 8192), (16, 512, 16384), (8, 256, 4096), (8, 512, 0), (8, 2048, 0))
 
 
@@ -327,13 +436,16 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--q-f32", action="store_true", help="prefill mode: f32 q (the reference's prefill arithmetic)")
     ap.add_argument("--valid", type=int, default=32768, help="decode mode: valid length (config 2)")
-    ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "decode", "ragged", "chunked"], default="bench",
+    ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "decode", "ragged", "chunked", "floor"],
+                    default="bench",
                     help="pmc: only a 256 MiB device copy and the config-2 split kernel, "
                          "5 launches each, for rocprofv3 --pmc runs; prefill: only config-4 "
                          "prefill at S=8192 (--steps calls), for kernel traces; decode: only "
                          "config-2 decode at --valid (--steps calls), for kernel traces; ragged: only "
                          "config-5 ragged decode (--steps calls), for kernel traces; chunked: "
-                         "only the split-key prefill shapes (--steps calls each), for kernel traces")
+                         "only the split-key prefill shapes (--steps calls each), for kernel traces; "
+                         "floor: the machine-floor probes (empty node, plain 64 MiB read, read + dependent "
+                         "node) beside the config-2 split kernel and call")
     args = ap.parse_args()
     if args.gpus != 1:
         print("this build measures one GPU only: the decode/prefill kernels run on a single "
@@ -367,6 +479,8 @@ def main() -> int:
         return ragged_mode(torch, backend, dev, max(1, min(args.steps, 500)))
     if args.mode == "chunked":
         return chunked_mode(torch, backend, dev, max(1, min(args.steps, 200)))
+    if args.mode == "floor":
+        return floor_mode(torch, backend, dev, max(10, min(args.steps, 2000)), max(1, min(args.warmup, 200)))
 
     def fixed_case(case, cap):
         cache = KVCache(cap, case.k.shape[1], case.k.shape[2], dev)

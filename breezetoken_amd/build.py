@@ -16,6 +16,9 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libbreezetoken_amd.so"
+# Machine-floor probes for bench.py --mode floor (not part of the attention ABI).
+PROBE_SRC = PKG / "probes" / "floor.hip"
+PROBE_LIB = PKG / "libbt_floor.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -49,22 +52,30 @@ def _compile(src: Path, obj: Path) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile all kernels and link ``libbreezetoken_amd.so``; returns its path."""
-    srcs = sorted(CSRC.glob("*.hip"))
-    objdir = PKG / "_build"
-    objdir.mkdir(exist_ok=True)
-    objs = [objdir / (s.stem + ".o") for s in srcs]
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        list(ex.map(lambda so: _compile(*so), zip(srcs, objs)))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs: list[Path], lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile all kernels and link ``libbreezetoken_amd.so`` (and the floor
+    probes' ``libbt_floor.so``); returns the attention library's path."""
+    srcs = sorted(CSRC.glob("*.hip"))
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    objs = [objdir / (s.stem + ".o") for s in srcs]
+    probe_obj = objdir / "floor_probe.o"
+    jobs = list(zip(srcs, objs)) + [(PROBE_SRC, probe_obj)]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+        list(ex.map(lambda so: _compile(*so), jobs))
+    _link(objs, LIB)
+    _link([probe_obj], PROBE_LIB)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIB} from {len(srcs)} sources, and {PROBE_LIB.name}", file=sys.stderr)
     return LIB
 
 
