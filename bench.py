@@ -359,11 +359,13 @@ def chunked_mode(torch, backend, dev, calls: int) -> int:
     return 0
 
 
-def decode_mode(torch, backend, dev, calls: int, valid: int) -> int:
+def decode_mode(torch, backend, dev, calls: int, valid: int, graph: bool = False) -> int:
     """Config-2 fixed-capacity decode at one valid length only (for rocprofv3
     kernel traces of split vs combine): ``calls`` calls rotating over six layer
     caches (384 MiB, past the MALL) after two warm-up rounds, timed with HIP
-    events on the current stream."""
+    events on the current stream.  Eager launches by default (the host's launch
+    gaps leave the GPU idle between calls); ``graph``: the six calls captured in
+    one hipGraph and replayed, as the headline times them."""
     from breezetoken_amd import workloads as wl
     from breezetoken_amd.kvcache import KVCache
 
@@ -381,6 +383,12 @@ def decode_mode(torch, backend, dev, calls: int, valid: int) -> int:
         _, k, v = layers[i % 6]
         backend.attention_fixed(q, k, v, pos, case.scale)
     torch.cuda.synchronize()
+    if graph:
+        six = lambda: [backend.attention_fixed(q, k, v, pos, case.scale) for _, k, v in layers]  # noqa: E731
+        us = time_graph(torch, six, max(1, calls // 6), 2) * 1e3 / 6  # one replay = six calls
+        print(json.dumps({"mode": "decode", "valid": valid, "calls": 6 * max(1, calls // 6), "us_per_call_graph": round(us, 2),
+                          "num_split": backend.pick_splits(case.k.shape[1], cap)}), flush=True)
+        return 0
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(torch.cuda.current_stream())
     for i in range(calls):
@@ -436,6 +444,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--q-f32", action="store_true", help="prefill mode: f32 q (the reference's prefill arithmetic)")
     ap.add_argument("--valid", type=int, default=32768, help="decode mode: valid length (config 2)")
+    ap.add_argument("--graph", action="store_true", help="decode mode: replay the calls in a hipGraph")
     ap.add_argument("--mode", choices=["bench", "pmc", "prefill", "decode", "ragged", "chunked", "floor"],
                     default="bench",
                     help="pmc: only a 256 MiB device copy and the config-2 split kernel, "
@@ -474,7 +483,7 @@ def main() -> int:
     if args.mode == "prefill":
         return prefill_mode(torch, backend, dev, max(1, min(args.steps, 200)), args.q_f32, min(args.warmup, 200))
     if args.mode == "decode":
-        return decode_mode(torch, backend, dev, max(1, min(args.steps, 2000)), args.valid)
+        return decode_mode(torch, backend, dev, max(1, min(args.steps, 2000)), args.valid, args.graph)
     if args.mode == "ragged":
         return ragged_mode(torch, backend, dev, max(1, min(args.steps, 500)))
     if args.mode == "chunked":
