@@ -313,8 +313,11 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // The softmax of q-tiles kNow.. is deferred to sm_tail, which runs in the
   // P.V phase: that phase (MFMAs and V^T reads) has slack, while Q.K^T +
   // softmax is each step's critical path.  Their masked scores wait in xd and
-  // the step's scale exponents in the *_d scalars.
-  constexpr int kNow = 1;
+  // the step's scale exponents in the *_d scalars.  Two q-tiles: the second
+  // is deferred (deferring both: C4 S = 8192 275.5 -> 281 us).  One q-tile
+  // (f32 q, whose Q.K^T issues two MFMAs per K fragment): it is deferred
+  // (426 -> 403 us, same results).
+  constexpr int kNow = NQT == 1 ? 0 : 1;
   u32x4 pk[NQT];
   float xd[NQT > kNow ? NQT - kNow : 1][8];
   int shift_d = 0, ek_d = 0, eold_d = 0, enew_d = 0;
