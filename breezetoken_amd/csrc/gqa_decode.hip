@@ -42,6 +42,11 @@ namespace {
 
 __device__ __forceinline__ int swz(int row, int slots) { return ((row & 7) * 2) & (slots - 1); }
 
+template <int V>
+struct IntConst {
+  static constexpr int value = V;
+};
+
 // Raw buffer resource over [base, base + bytes): loads past the end return 0,
 // so tokens past the valid length need no clamping.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -435,51 +440,61 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   }
   __syncthreads();
 
-  // Each thread finishes (head, 4 consecutive d) items.
-  for (int item = threadIdx.x; item < G * (D / 4); item += kThreads) {
-    const int h = item / (D / 4);
-    const int d = (item % (D / 4)) * 4;
-    // Every LDS read is issued before the first use and the weights are a
-    // select, not a branch (a branch per wave made each l read its own LDS
-    // round trip).  A wave without valid tokens has l = 0, m = -inf and a zero
-    // partial: its weight is 0 (the exp2 of its NaN difference is discarded).
-    float mw[W], lw[W];
-    float4 ow[W];
+  // Each thread finishes (head, 4 consecutive d) items, over the first NW
+  // waves' partials: the waves dealt a tile of this split (wave w's first tile
+  // is s + ns_eff * w), rounded up to 2, 4 or W.  The others' partials are
+  // zeros with weight 0 and are not read (C2 1k / 4k -0.15 / -0.19 us).
+  auto merge = [&](auto nw) {
+    constexpr int NW = decltype(nw)::value;
+    for (int item = threadIdx.x; item < G * (D / 4); item += kThreads) {
+      const int h = item / (D / 4);
+      const int d = (item % (D / 4)) * 4;
+      // Every LDS read is issued before the first use and the weights are a
+      // select, not a branch (a branch per wave made each l read its own LDS
+      // round trip).  A wave without valid tokens has l = 0, m = -inf and a
+      // zero partial: its weight is 0 (the exp2 of its NaN difference is
+      // discarded).
+      float mw[NW], lw[NW];
+      float4 ow[NW];
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
-      mw[w] = mm[w * GMAX + h];
-      lw[w] = ml[w * GMAX + h];
-      ow[w] = *reinterpret_cast<const float4*>(mlds + (w * GMAX + h) * kMoStride + d);
+      for (int w = 0; w < NW; ++w) {
+        mw[w] = mm[w * GMAX + h];
+        lw[w] = ml[w * GMAX + h];
+        ow[w] = *reinterpret_cast<const float4*>(mlds + (w * GMAX + h) * kMoStride + d);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) mx = fmaxf(mx, mw[w]);
+      float lsum = 0.f;
+      float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float e = fast_exp2(mw[w] - mx);
+        const float sc = lw[w] > 0.f ? e : 0.f;
+        lsum += lw[w] * sc;
+        acc.x += ow[w].x * sc; acc.y += ow[w].y * sc; acc.z += ow[w].z * sc; acc.w += ow[w].w * sc;
+      }
+      const int64_t row = (int64_t)(head0 + h) * p.total_splits + split_idx;
+      // The partial is stored unconditionally (zeros for a split without
+      // valid tokens, whose lse of -inf the combine skips), so the compiler
+      // cannot sink its LDS reads behind the weights' into a second round trip.
+      const bool has = lsum > 0.f;
+      const float inv = has ? 1.f / lsum : 0.f;
+      acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
+      *reinterpret_cast<float4*>(p.part + row * D + d) = acc;
+      if (d == 0) p.lse[row] = has ? fast_log2(lsum) + mx : -INFINITY;
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < W; ++w) mx = fmaxf(mx, mw[w]);
-    float lsum = 0.f;
-    float4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const float e = fast_exp2(mw[w] - mx);
-      const float sc = lw[w] > 0.f ? e : 0.f;
-      lsum += lw[w] * sc;
-      acc.x += ow[w].x * sc; acc.y += ow[w].y * sc; acc.z += ow[w].z * sc; acc.w += ow[w].w * sc;
-    }
-    const int64_t row = (int64_t)(head0 + h) * p.total_splits + split_idx;
-    // The partial is stored unconditionally (zeros for a split without valid
-    // tokens, whose lse of -inf the combine skips), so the compiler cannot
-    // sink its LDS reads behind the weights' into a second round trip.
-    const bool has = lsum > 0.f;
-    const float inv = has ? 1.f / lsum : 0.f;
-    acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
-    *reinterpret_cast<float4*>(p.part + row * D + d) = acc;
-    if (d == 0) p.lse[row] = has ? fast_log2(lsum) + mx : -INFINITY;
+  };
+  if constexpr (W > 4) {
+    // Wave w has a tile iff s + ns_eff * w < tiles.
+    if (s + 2 * ns_eff >= tiles) merge(IntConst<2>{});
+    else if (s + 4 * ns_eff >= tiles) merge(IntConst<4>{});
+    else merge(IntConst<W>{});
+  } else {
+    merge(IntConst<W>{});
   }
 }
 
-namespace {
-
-
-
-}  // namespace
 
 // LSE combine (attention.py:168-189).  One wave per (head, sequence,
 // 8-column chunk): lane = (split group lane >> 1, float4 column lane & 1).
