@@ -369,7 +369,21 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       for (int i = 0; i < kDTiles; ++i) oacc[t][i] *= alpha;
     }
   };
-  auto qk_sm = [&](const unsigned char* kb, int u, int eb, int ek) {
+  // K fragment (d-step st, key tile kt) of the K tile kb.
+  auto kread_at = [&](const unsigned char* kb, int st, int kt) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(kb + kaddr[st & 3] + (st & 4) * 64 + kt * 16 * kRowBytes);
+  };
+  // The first kKLead d-steps' K fragments, read right after the barrier that
+  // publishes the tile (before the step's tile copies are issued), so their
+  // LDS latency overlaps the copies' issue.
+  auto k_first = [&](const unsigned char* kb, u32x4 (&kf)[kKLead + 1][2]) {
+#pragma unroll
+    for (int i = 0; i < kKLead; ++i) {
+      kf[i][0] = kread_at(kb, i, 0);
+      kf[i][1] = kread_at(kb, i, 1);
+    }
+  };
+  auto qk_sm = [&](const unsigned char* kb, int u, int eb, int ek, u32x4 (&kf)[kKLead + 1][2]) {
     const int blk = unit_blk(u);
     const int key0 = unit_key(u) * kUnit;
     floatx4 sacc[2][NQT];
@@ -380,16 +394,8 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     // K fragments are read kKLead d-steps ahead of their MFMAs (scheduling
     // barriers keep the compiler from hoisting all of them: the registers are
     // spoken for by O and Q).
-    auto kread = [&](int st, int kt) -> u32x4 {
-      return *reinterpret_cast<const u32x4*>(kb + kaddr[st & 3] + (st & 4) * 64 + kt * 16 * kRowBytes);
-    };
+    auto kread = [&](int st, int kt) -> u32x4 { return kread_at(kb, st, kt); };
     constexpr int KLA = kKLead;
-    u32x4 kf[KLA + 1][2];
-#pragma unroll
-    for (int i = 0; i < KLA; ++i) {
-      kf[i][0] = kread(i, 0);
-      kf[i][1] = kread(i, 1);
-    }
 #pragma unroll
     for (int st = 0; st < kDSteps; ++st) {
       if (st + KLA < kDSteps) {
@@ -526,14 +532,16 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     const bool w0 = working(st), w1 = working(st + 1);
     // The wave running Q.K^T + softmax gets issue priority, so its MFMAs go
     // first and its softmax overlaps the other wave's P.V.
+    u32x4 kf[kKLead + 1][2];
     if constexpr (GRP == 0) {
       wait_tiles(1);  // K of st (its V^T was issued after it)
       barrier();
+      if (w0) k_first(Kc, kf);
       int eb_n, ek_n;
       unit_scales(st + 1, eb_n, ek_n);
       if (w1) { copy_k(Kn, st + 1); copy_v(Vn, st + 1); }
       __builtin_amdgcn_s_setprio(1);
-      if (w0) qk_sm(Kc, st, eb, ek);
+      if (w0) qk_sm(Kc, st, eb, ek, kf);
       __builtin_amdgcn_s_setprio(0);
       eb = eb_n;
       ek = ek_n;
@@ -549,9 +557,10 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       if (working(st - 1)) pv(Vn);
       wait_tiles((w0 ? 1 : 0) + (w1 ? 1 : 0));  // K of st (behind it: V^T of st, K of st + 1)
       barrier();
+      if (w0) k_first(Kc, kf);
       if (w1) copy_v(Vn, st + 1);
       __builtin_amdgcn_s_setprio(1);
-      if (w0) qk_sm(Kc, st, eb, ek);
+      if (w0) qk_sm(Kc, st, eb, ek, kf);
       __builtin_amdgcn_s_setprio(0);
       eb = eb_n;
       ek = ek_n;
