@@ -368,15 +368,22 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     // S^T (64 keys x 16 queries) = K . Q^T from K buffer b: A operand of d-step
     // st / key sub-tile sub is chunk st*4 + g4 of key row sub*16 + i16, stored
     // in slot (st*4 + g4) ^ i16 of that row (row & 15 == i16).
-    auto qk = [&](auto b, floatx4 (&sacc)[4]) {
-      const unsigned char* kb_ = k_buf(b);
+    auto kfrag = [&](auto b, int st, int sub) -> u32x4 {
+      return *reinterpret_cast<const u32x4*>(k_buf(b) + (sub * 16 + i16) * (D * 2) + (((st * 4 + g4) ^ i16) * 16));
+    };
+    // The first d-step's K fragments, read right after the barrier that
+    // publishes the tile, ahead of the tile copies the step issues.
+    auto k_first = [&](auto b, u32x4 (&f0)[4]) {
+  #pragma unroll
+      for (int sub = 0; sub < 4; ++sub) f0[sub] = kfrag(b, 0, sub);
+    };
+    auto qk = [&](auto b, floatx4 (&sacc)[4], const u32x4 (&f0)[4]) {
       const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
   #pragma unroll
       for (int st = 0; st < kDSteps; ++st) {
   #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(kb_ + (sub * 16 + i16) * (D * 2) +
-                                                            (((st * 4 + g4) ^ i16) * 16));
+          const u32x4 a = st == 0 ? f0[sub] : kfrag(b, st, sub);
           sacc[sub] = mfma16_f16(a, qop[st], st == 0 ? zero : sacc[sub]);
           if constexpr (LO) sacc[sub] = mfma16_f16(a, qlo[st], sacc[sub]);
         }
@@ -457,7 +464,11 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     __syncthreads();
     {
       floatx4 sacc[4];
-      qk(Buf8<0>{}, sacc);
+      {
+        u32x4 f0[4];
+        k_first(Buf8<0>{}, f0);
+        qk(Buf8<0>{}, sacc, f0);
+      }
       barrier();
       if (kb0 + 2 <= last) copy_k(Buf8<0>{}, kb0 + 2);
       if (kb0 >= kb_diag) mask(kb0, sacc);
@@ -473,11 +484,13 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     auto step = [&](auto b, int kb) {
       constexpr int B = decltype(b)::value;
       const bool second = kb == kb0 + 1;  // its V^T went out in the prologue
+      u32x4 f0[4];
+      k_first(b, f0);
       if (!second) copy_v(b, kb);
       int ek_n, eb_n;
       scales(kb + 1, ek_n, eb_n);
       floatx4 sacc[4];
-      qk(b, sacc);
+      qk(b, sacc, f0);
       // V_{kb-1}; issued after it: K_{kb+1} (if any) and V_kb (in the second
       // block: V_{kb0+1}, from the prologue).
       wait_tiles((kb + 1 <= last ? 1 : 0) + 1);
