@@ -372,7 +372,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       kf[i][1] = kread_at(kb, i, 1);
     }
   };
-  auto qk_sm = [&](const unsigned char* kb, int u, int eb, int ek, u32x4 (&kf)[kKLead + 1][2]) {
+  auto qk_sm = [&](const unsigned char* kb, int u, int eb, int ek, u32x4 (&kf)[kKLead + 1][2], auto&& after_mfma) {
     const int blk = unit_blk(u);
     const int key0 = unit_key(u) * kUnit;
     floatx4 sacc[2][NQT];
@@ -406,6 +406,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    after_mfma();
     // Causal mask: key key0 + kt*16 + g4*4 + r against this column's position.
     // The lane's column and lane group are re-derived here from the V^T
     // operand address (g4 * D * 16 + i16 * 16), which the loop keeps anyway,
@@ -527,10 +528,13 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       barrier();
       if (w0) k_first(Kc, kf);
       int eb_n, ek_n;
-      unit_scales(st + 1, eb_n, ek_n);
       if (w1) { copy_k(Kn, st + 1); copy_v(Vn, st + 1); }
       __builtin_amdgcn_s_setprio(1);
-      if (w0) qk_sm(Kc, st, eb, ek, kf);
+      // The next step's block scales are requested after the MFMAs: scalar
+      // loads share the LDS reads' counter and return out of order, so issued
+      // earlier they would hold the first MFMA until they arrive.
+      if (w0) qk_sm(Kc, st, eb, ek, kf, [&] { unit_scales(st + 1, eb_n, ek_n); });
+      else unit_scales(st + 1, eb_n, ek_n);
       __builtin_amdgcn_s_setprio(0);
       eb = eb_n;
       ek = ek_n;
@@ -541,7 +545,6 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       wait_tiles(w0 ? 2 : 0);  // V^T of st - 1 (behind it: K and V^T of st)
       barrier();
       int eb_n, ek_n;
-      unit_scales(st + 1, eb_n, ek_n);
       if (w1) copy_k(Kn, st + 1);
       if (working(st - 1)) pv(Vn);
       wait_tiles((w0 ? 1 : 0) + (w1 ? 1 : 0));  // K of st (behind it: V^T of st, K of st + 1)
@@ -549,7 +552,8 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       if (w0) k_first(Kc, kf);
       if (w1) copy_v(Vn, st + 1);
       __builtin_amdgcn_s_setprio(1);
-      if (w0) qk_sm(Kc, st, eb, ek, kf);
+      if (w0) qk_sm(Kc, st, eb, ek, kf, [&] { unit_scales(st + 1, eb_n, ek_n); });
+      else unit_scales(st + 1, eb_n, ek_n);
       __builtin_amdgcn_s_setprio(0);
       eb = eb_n;
       ek = ek_n;
