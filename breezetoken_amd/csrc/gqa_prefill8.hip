@@ -488,9 +488,12 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       k_first(b, f0);
       if (!second) copy_v(b, kb);
       int ek_n, eb_n;
-      scales(kb + 1, ek_n, eb_n);
       floatx4 sacc[4];
       qk(b, sacc, f0);
+      // The next block's scales are requested after the MFMAs: scalar loads
+      // share the LDS reads' counter and return out of order, so issued
+      // earlier they would hold the first MFMA until they arrive.
+      scales(kb + 1, ek_n, eb_n);
       // V_{kb-1}; issued after it: K_{kb+1} (if any) and V_kb (in the second
       // block: V_{kb0+1}, from the prologue).
       wait_tiles((kb + 1 <= last ? 1 : 0) + 1);
