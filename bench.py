@@ -285,7 +285,9 @@ def floor_mode(torch, backend, dev, steps: int, warmup: int) -> int:
     rows = nbytes // 1024
     for mode, key, nb_ in ((0, "read_half_rows_32MiB", nbytes // 2), (1, "read_rows_halves_adjacent_groups", nbytes),
                            (2, "read_rows_halves_one_group", nbytes),
-                           (3, "read_rows_halves_adjacent_groups_row_loads", nbytes)):
+                           (3, "read_rows_halves_adjacent_groups_row_loads", nbytes),
+                           (4, "read_rows_halves_adjacent_groups_quarter_row_loads", nbytes),
+                           (5, "read_rows_halves_adjacent_groups_quarter_row_loads_row_minor_lanes", nbytes)):
         us = time_graph(torch, lambda: [ok(fl.bt_floor_read_rows(b.data_ptr(), rows, 1024, mode, out.data_ptr(), st()))
                                         for b in bufs], steps, warmup) / 6
         res[key] = {"cold_us": round(us * 1e3, 3), "cold_GBps": round(nb_ / (us * 1e-3) / 1e9, 1)}

@@ -65,8 +65,8 @@ __global__ __launch_bounds__(256) void floor_read_lds(const void* src, uint32_t 
 }
 
 // The decode kernel's K pattern: token rows of `row_bytes` (the cache's token
-// stride), each 64-lane load covering 16 rows x 64 bytes (lanes 4t..4t+3 take
-// 16 bytes each of row t), LPT loads per thread stepping 64 bytes along the
+// stride), each 64-lane load covering 16 rows x 64 bytes (lanes t, t+16, t+32
+// and t+48 take 16 bytes each of row t), LPT loads per thread stepping 64 bytes along the
 // rows; a work-group covers 64 consecutive rows' first LPT * 64 bytes.
 // MODE 0: the first half of each row only, 64 rows per work-group; 1: both
 // halves, work-groups 2i and 2i+1 taking the two halves of the same 64 rows
@@ -79,16 +79,27 @@ __global__ __launch_bounds__(256) void floor_read_rows(const void* src, uint32_t
   const int wave = (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
   uint32_t row0, half;
   if constexpr (MODE == 0) { row0 = (uint32_t)blockIdx.x * 64 + wave * 16; half = 0; }
-  else if constexpr (MODE == 1 || MODE == 3) { row0 = (uint32_t)(blockIdx.x >> 1) * 64 + wave * 16; half = blockIdx.x & 1; }
+  else if constexpr (MODE == 1 || MODE >= 3) { row0 = (uint32_t)(blockIdx.x >> 1) * 64 + wave * 16; half = blockIdx.x & 1; }
   else { row0 = (uint32_t)blockIdx.x * 32 + (wave & 1) * 16; half = wave >> 1; }
   // MODE 3: each load covers two whole half-rows (lanes 0-31 row 2i, 32-63
-  // row 2i+1, 16 bytes each), the way the decode kernel copies V.
-  const uint32_t voff = MODE == 3 ? (row0 + (lane >> 5)) * row_bytes + half * (row_bytes / 2) + (lane & 31) * 16
-                                  : (row0 + (lane & 15)) * row_bytes + half * (row_bytes / 2) + (lane >> 4) * 16;
-  const uint32_t step = MODE == 3 ? 2 * row_bytes : 64;
+  // row 2i+1, 16 bytes each), the way the decode kernel copies V.  MODE 4:
+  // each load covers 256 contiguous bytes of four rows (lanes 16t..16t+15 row
+  // t), loads 2j and 2j+1 the two quarters of rows 4j..4j+3.  MODE 5: as 4
+  // with lane l on row l % 4 (16-byte chunk l / 4), the operand layout of the
+  // 4x4x4 block MFMA.
+  uint32_t voff;
+  if constexpr (MODE == 3) voff = (row0 + (lane >> 5)) * row_bytes + half * (row_bytes / 2) + (lane & 31) * 16;
+  else if constexpr (MODE == 4) voff = (row0 + (lane >> 4)) * row_bytes + half * (row_bytes / 2) + (lane & 15) * 16;
+  else if constexpr (MODE == 5) voff = (row0 + (lane & 3)) * row_bytes + half * (row_bytes / 2) + (lane >> 2) * 16;
+  else voff = (row0 + (lane & 15)) * row_bytes + half * (row_bytes / 2) + (lane >> 4) * 16;
+  auto step = [&](int i) -> uint32_t {
+    if constexpr (MODE == 3) return i * 2 * row_bytes;
+    else if constexpr (MODE == 4 || MODE == 5) return (i >> 1) * 4 * row_bytes + (i & 1) * 256;
+    else return i * 64;
+  };
   u32x4 v[LPT];
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(voff + i * step), 0, kPolicyStream);
+  for (int i = 0; i < LPT; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(voff + step(i)), 0, kPolicyStream);
   uint32_t x = 0;
 #pragma unroll
   for (int i = 0; i < LPT; ++i) x ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
@@ -141,11 +152,13 @@ int bt_floor_read_lds(const void* src, int64_t bytes, uint32_t* out, void* strea
 // stride.  `out` holds one word per work-group (rows / 64).
 // mode 1 / 2: both halves of every row of 1,024 bytes (row_bytes must be 1024),
 // read by adjacent work-groups (1) or inside one work-group (2); mode 3: as 1,
-// each load covering two whole half-rows.  `out` holds
-// one word per work-group (rows / 64, rows / 32 or rows / 32).
+// each load covering two whole half-rows; mode 4: as 1, each load covering 256
+// contiguous bytes of four rows (lanes 16t..16t+15 on row t); mode 5: as 4,
+// lane l on row l % 4.  `out` holds one word per work-group (rows /
+// 64 for mode 0, rows / 32 otherwise).
 int bt_floor_read_rows(const void* src, int64_t rows, int64_t row_bytes, int32_t mode, uint32_t* out, void* stream) {
   if (!src || !out || rows <= 0 || rows % 64 || row_bytes < 512 || row_bytes % 16 ||
-      rows * row_bytes > (1LL << 31) || mode < 0 || mode > 3 || (mode > 0 && row_bytes != 1024))
+      rows * row_bytes > (1LL << 31) || mode < 0 || mode > 5 || (mode > 0 && row_bytes != 1024))
     return (int)hipErrorInvalidValue;
   const hipStream_t st = (hipStream_t)stream;
   const uint32_t rb = (uint32_t)row_bytes;
@@ -153,6 +166,8 @@ int bt_floor_read_rows(const void* src, int64_t rows, int64_t row_bytes, int32_t
   if (mode == 1) hipLaunchKernelGGL((floor_read_rows<8, 1>), dim3((unsigned)(rows / 32)), dim3(256), 0, st, src, rb, out);
   if (mode == 2) hipLaunchKernelGGL((floor_read_rows<8, 2>), dim3((unsigned)(rows / 32)), dim3(256), 0, st, src, rb, out);
   if (mode == 3) hipLaunchKernelGGL((floor_read_rows<8, 3>), dim3((unsigned)(rows / 32)), dim3(256), 0, st, src, rb, out);
+  if (mode == 4) hipLaunchKernelGGL((floor_read_rows<8, 4>), dim3((unsigned)(rows / 32)), dim3(256), 0, st, src, rb, out);
+  if (mode == 5) hipLaunchKernelGGL((floor_read_rows<8, 5>), dim3((unsigned)(rows / 32)), dim3(256), 0, st, src, rb, out);
   return (int)hipGetLastError();
 }
 
