@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X GQA attention path (one GPU).
 
-Headline (BASELINE.json ``metric``, config 2): split-KV GQA flash-decode,
+Headline (decode µs per call and HBM GB/s, config 2): split-KV GQA flash-decode,
 Qwen3.5-0.8B-like H=8 / Hkv=2 / D=256, bf16 fixed-capacity cache of 65,536
 slots, valid length 32,768 given by a device position tensor, q/K/V ~ N(0, 1)
 bf16 (seed 1).  One step = one decode call (split + LSE combine).  The calls

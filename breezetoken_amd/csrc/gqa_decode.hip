@@ -501,10 +501,11 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
 // Each lane fetches the partials and LSEs of its splits in one batch; the max
 // and the sums over the 32 split groups are lane shuffles, so the kernel makes
 // one memory round trip before its store and has no barrier (splits past the
-// first 32*kPre take a slower second pass).  Per config-2 call at 32k this
-// took 17.05 us, against 17.17 us with 16 groups x 4 columns, 17.18 us with
-// 64 groups x 1 column, and 17.68 us for a 256-thread work-group per
-// 64-column chunk with LDS reductions.
+// first 32*kPre take a slower second pass).  When this layout was chosen, a
+// config-2 call at 32k (split kernel of that time included) took 17.05 us
+// with it, against 17.17 us with 16 groups x 4 columns, 17.18 us with 64
+// groups x 1 column, and 17.68 us for a 256-thread work-group per 64-column
+// chunk with LDS reductions.
 template <int D, bool RAGGED, int GROUPS>
 __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p) {
   static_assert(GROUPS >= 1 && GROUPS <= 64 && (GROUPS & (GROUPS - 1)) == 0,

@@ -1,6 +1,6 @@
 """GPU parity of the split-KV decode kernels against the CPU oracle.
 
-Gate (BASELINE north star): max-abs error <= 2e-3 and cosine similarity
+Gate: max-abs error <= 2e-3 and cosine similarity
 >= 0.99999 against the torch f32 reference attention on the same bf16-rounded
 inputs.  Every call goes through libbreezetoken_amd.so.
 """
