@@ -48,9 +48,12 @@ __device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) {
   return (lo16 & 0xffffu) | (hi16 << 16);
 }
 
+// Lane permutation for controls whose every source lane exists (the row
+// mirrors): bound_ctrl then changes no value, and with it set the compiler
+// folds the move into the VALU instruction that consumes it (v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, true));
 }
 
 __device__ __forceinline__ floatx4 mfma16(const bf16x8& a, const bf16x8& b, const floatx4& c) {
