@@ -113,23 +113,24 @@ __device__ __forceinline__ float halves_sum(float x) {
 }
 
 // op(x, x[l ^ MASK]) for one butterfly step of a commutative op on 32-bit
-// lanes, without an LDS round trip: DPP for MASK 1 and 2 (quad permutes) and
-// 4 and 8 (row shifts, the two halves of each pair of banks taking opposite
-// directions), lane swaps for 16 and 32.  The op sees the lane's own value and
-// its partner's, so the result equals op(x, __shfl_xor(x, MASK)) bit for bit.
+// lanes, without an LDS round trip: DPP for MASK 1 and 2 (quad permutes), 4
+// (row shifts, the two halves of each pair of banks taking opposite
+// directions) and 8 (a row rotation by 8), lane swaps for 16 and 32.  The op
+// sees the lane's own value and its partner's, so the result equals op(x,
+// __shfl_xor(x, MASK)) bit for bit.  Where one DPP move with every source lane
+// present does the permute (MASK 1, 2, 8), bound_ctrl is set: it changes no
+// value and lets the compiler fold the move into the op that consumes it.
 template <int MASK>
 __device__ __forceinline__ uint32_t xor_partner_bits(uint32_t x) {
   const int v = (int)x;
-  if constexpr (MASK == 1) return (uint32_t)__builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
-  if constexpr (MASK == 2) return (uint32_t)__builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+  if constexpr (MASK == 1) return (uint32_t)__builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, true);  // quad_perm 1,0,3,2
+  if constexpr (MASK == 2) return (uint32_t)__builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, true);  // quad_perm 2,3,0,1
   if constexpr (MASK == 4) {  // banks 0, 2 read lane + 4 (row_shl:4), banks 1, 3 lane - 4 (row_shr:4)
     const int lo = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0x5, false);
     return (uint32_t)__builtin_amdgcn_update_dpp(lo, v, 0x114, 0xf, 0xA, false);
   }
-  if constexpr (MASK == 8) {  // banks 0, 1 read lane + 8 (row_shl:8), banks 2, 3 lane - 8 (row_shr:8)
-    const int lo = __builtin_amdgcn_update_dpp(0, v, 0x108, 0xf, 0x3, false);
-    return (uint32_t)__builtin_amdgcn_update_dpp(lo, v, 0x118, 0xf, 0xC, false);
-  }
+  // row_ror:8: lane l of a row of 16 reads lane (l + 8) mod 16 = l ^ 8.
+  if constexpr (MASK == 8) return (uint32_t)__builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, true);
   static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "xor_partner_bits: 1, 2, 4 or 8");
   return x;
 }
