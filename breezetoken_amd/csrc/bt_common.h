@@ -44,6 +44,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
+// Two floats -> two bf16 packed in one word (a in the low half), round to
+// nearest even, by the hardware conversion (v_cvt_pk_bf16_f32): with f32
+// denormals kept (the kernels' default float mode) the same bits as
+// f32_to_bf16_bits for every finite or infinite input.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
 __device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) {
   return (lo16 & 0xffffu) | (hi16 << 16);
 }

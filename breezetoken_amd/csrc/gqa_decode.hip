@@ -189,8 +189,15 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
     col_lo = true;
   }
   // Branch-free operand selection: keep_hi / keep_lo are all-ones or zero.
-  const uint32_t keep_hi = (col_head >= 0 && !col_lo) ? 0xffffu : 0u;
-  const uint32_t keep_lo = col_lo ? 0xffffu : 0u;
+  const uint32_t keep_hi = (col_head >= 0 && !col_lo) ? 0xffffffffu : 0u;
+  const uint32_t keep_lo = col_lo ? 0xffffffffu : 0u;
+  // Two values as bf16 hi = rne(x) and lo = rne(x - hi), packed: the hi
+  // columns take hi, the lo columns lo, the others zero.
+  auto hilo2 = [&](float a, float b) -> uint32_t {
+    const uint32_t hi = f32x2_to_bf16x2_bits(a, b);
+    const uint32_t lo = f32x2_to_bf16x2_bits(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+    return (hi & keep_hi) | (lo & keep_lo);
+  };
 
   // ---- q first: wave w < kSteps loads the q slice of d-step w at entry ------
   // (a wave's loads complete in issue order, so q must not queue behind K/V).
@@ -289,16 +296,10 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
         qv[4 + i] = __uint_as_float(qraw[1][i]);
       }
     }
-    uint32_t h16[8];
+    u32x4 qw;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float x = qv[i] * p.scale_log2;
-      const uint32_t hi = f32_to_bf16_bits(x);
-      const uint32_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
-      h16[i] = (hi & keep_hi) | (lo & keep_lo);
-    }
-    qlds[wave * 64 + lane] = u32x4{pack2(h16[0], h16[1]), pack2(h16[2], h16[3]), pack2(h16[4], h16[5]),
-                                   pack2(h16[6], h16[7])};
+    for (int i = 0; i < 4; ++i) qw[i] = hilo2(qv[2 * i] * p.scale_log2, qv[2 * i + 1] * p.scale_log2);
+    qlds[wave * 64 + lane] = qw;
   }
   // The first tile's loads go out after the Q^T build: issued before it, they
   // would sit behind q in the wave's load queue on one path and not on the
@@ -388,14 +389,7 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
       for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
     }
     // P^T operand: this lane's own probabilities, as bf16 hi or lo.
-    uint32_t p16[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t hi = f32_to_bf16_bits(pr[j]);
-      const uint32_t lo = f32_to_bf16_bits(pr[j] - bf16_bits_to_f32(hi));
-      p16[j] = (hi & keep_hi) | (lo & keep_lo);
-    }
-    const u32x2 pop = {pack2(p16[0], p16[1]), pack2(p16[2], p16[3])};
+    const u32x2 pop = {hilo2(pr[0], pr[1]), hilo2(pr[2], pr[3])};
 
     // O^T += V^T . P^T, V^T read transposed from LDS.
     u32x2 vop[kDTiles];
@@ -589,8 +583,7 @@ __global__ __launch_bounds__(64) void gqa_decode_combine_kernel(CombineParams p)
     const int64_t orow = (int64_t)b * p.out_stride_seq + (int64_t)h * D + chunk * 4 * kCols + t * 4;
     if (p.out_bf16) {
       uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + orow;
-      const u32x2 pk = {pack2(f32_to_bf16_bits(acc.x), f32_to_bf16_bits(acc.y)),
-                        pack2(f32_to_bf16_bits(acc.z), f32_to_bf16_bits(acc.w))};
+      const u32x2 pk = {f32x2_to_bf16x2_bits(acc.x, acc.y), f32x2_to_bf16x2_bits(acc.z, acc.w)};
       *reinterpret_cast<u32x2*>(o) = pk;
     } else {
       *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow) = acc;

@@ -554,8 +554,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
         const int d = dt * 16 + g4 * 4;
         const float o0 = oacc[dt][0] * inv, o1 = oacc[dt][1] * inv, o2 = oacc[dt][2] * inv, o3 = oacc[dt][3] * inv;
         if (p.out_bf16) {
-          const u32x2 pk2 = {pack2(f32_to_bf16_bits(o0), f32_to_bf16_bits(o1)),
-                             pack2(f32_to_bf16_bits(o2), f32_to_bf16_bits(o3))};
+          const u32x2 pk2 = {f32x2_to_bf16x2_bits(o0, o1), f32x2_to_bf16x2_bits(o2, o3)};
           *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
         } else {
           *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = float4{o0, o1, o2, o3};
@@ -668,8 +667,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
   const int head = (ysub / p.head_subs) * p.group + (ysub % p.head_subs) * G + w % G;
   const int64_t orow = (int64_t)q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
   if (p.out_bf16) {
-    const u32x2 pk2 = {pack2(f32_to_bf16_bits(acc.x), f32_to_bf16_bits(acc.y)),
-                       pack2(f32_to_bf16_bits(acc.z), f32_to_bf16_bits(acc.w))};
+    const u32x2 pk2 = {f32x2_to_bf16x2_bits(acc.x, acc.y), f32x2_to_bf16x2_bits(acc.z, acc.w)};
     *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
   } else {
     *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = acc;

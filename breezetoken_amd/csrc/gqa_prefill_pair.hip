@@ -284,8 +284,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
         const float o0 = oacc[t][dt][0] * inv, o1 = oacc[t][dt][1] * inv, o2 = oacc[t][dt][2] * inv,
                     o3 = oacc[t][dt][3] * inv;
         if (p.out_bf16) {
-          const u32x2 pk2 = {pack2(f32_to_bf16_bits(o0), f32_to_bf16_bits(o1)),
-                             pack2(f32_to_bf16_bits(o2), f32_to_bf16_bits(o3))};
+          const u32x2 pk2 = {f32x2_to_bf16x2_bits(o0, o1), f32x2_to_bf16x2_bits(o2, o3)};
           *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
         } else {
           *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = float4{o0, o1, o2, o3};
