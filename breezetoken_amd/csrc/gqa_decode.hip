@@ -155,16 +155,25 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   // a cache row, and work-groups dispatched together then read both halves of
   // the same rows at about the same time, which the DRAM serves better (C2 32k
   // -0.2 us per call, C3 32k -0.6 us, C5 -1.0 us against one grid row per head).
-  const int kvh = (int)blockIdx.x % p.kv_heads;
+  // A power-of-two Hkv (every served model) splits x with a mask and a shift
+  // instead of a division, which would sit before the first loads.
+  int kvh, xq;
+  if ((p.kv_heads & (p.kv_heads - 1)) == 0) {
+    kvh = (int)blockIdx.x & (p.kv_heads - 1);
+    xq = (int)blockIdx.x >> __builtin_ctz((unsigned)p.kv_heads);
+  } else {
+    kvh = (int)blockIdx.x % p.kv_heads;
+    xq = (int)blockIdx.x / p.kv_heads;
+  }
   const int G = p.group;
 
   int b, s, ns, base;
   if constexpr (MODE == kModeRagged) {
-    const int* w = reinterpret_cast<const int*>(p.work) + 4 * ((int)blockIdx.x / p.kv_heads);
+    const int* w = reinterpret_cast<const int*>(p.work) + 4 * xq;
     b = uniform_load(w, 0); s = uniform_load(w, 1); ns = uniform_load(w, 2); base = uniform_load(w, 3);
     if (b < 0) return;  // padding entry of a device-built plan
   } else {
-    b = blockIdx.z; s = (int)blockIdx.x / p.kv_heads; ns = p.num_split; base = b * p.num_split;
+    b = blockIdx.z; s = xq; ns = p.num_split; base = b * p.num_split;
   }
   // The length source is read first so its round trip overlaps the q loads.
   int len_raw;
@@ -269,7 +278,9 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   int ns_eff = ns;
   if constexpr (MODE != kModeRagged) {
     if (p.tiles_per_split > 0) {
-      const int want = (tiles + p.tiles_per_split - 1) / p.tiles_per_split;
+      int want;
+      if (p.tiles_per_split == kDecodeTilesPerSplit) want = (tiles + kDecodeTilesPerSplit - 1) / kDecodeTilesPerSplit;
+      else want = (tiles + p.tiles_per_split - 1) / p.tiles_per_split;
       ns_eff = want < 1 ? 1 : (want < ns ? want : ns);
     }
   }
@@ -279,7 +290,6 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   }
   const int tstride = ns_eff * W;                       // tile distance between a wave's steps
   const int tfirst = s + ns_eff * wave;                 // this wave's first tile
-  const int my_tiles = tfirst < tiles ? (tiles - tfirst + tstride - 1) / tstride : 0;
   // ---- Q^T operand (bf16 hi or lo of q*scale*log2e): wave w builds d-step w.
   if (wave < kSteps) {
     float qv[8];
@@ -306,7 +316,7 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   // other (a wave without tiles), and the compiler's wait for q would then be
   // for every load -- the wave's first tile, and through the barrier the
   // slowest wave's.  q and pos arrive about together, so this costs little.
-  if (my_tiles > 0 && !spec_loaded) {
+  if (tfirst < tiles && !spec_loaded) {
     issue_k(tfirst);
     issue_v(tfirst);
   }
@@ -322,9 +332,9 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
   const int i16 = lane & 15;
   const int row1 = 4 * kg + (i16 >> 2);  // V^T read: token row of this lane
 
-  for (int it = 0; it < my_tiles; ++it) {
-    const int tile = tfirst + it * tstride;
-    const bool more = it + 1 < my_tiles;
+  for (int it = 0, tile = tfirst; tile < tiles; ++it, tile += tstride) {
+    const bool first = it == 0;
+    const bool more = tile + tstride < tiles;
     // S^T = K . Q^T.
     floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
     u32x4 qop[kSteps];
@@ -337,12 +347,12 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
     // exact (each MFMA waits for its own K load) without the next requests
     // joining the queue while the first V is still arriving (4k -0.2 us,
     // C3 32k -0.18 us, 32k -0.08 us; issued late in every step, 131k +0.9 us).
-    if (more && it > 0) issue_k(tile + tstride);
+    if (more && !first) issue_k(tile + tstride);
     // Stage V in this wave's swizzled LDS tile (same-wave LDS ops stay
     // ordered) and request the next V.  Rows past the valid length are zeros
     // (buffer range), except in a speculative tile read inside the capacity:
     // there they are zeroed here, since p = 0 on them but 0 * NaN is not 0.
-    const bool spec_tail = kSpec && it == 0 && spec_loaded && tile * 16 + 16 > valid;
+    const bool spec_tail = kSpec && first && spec_loaded && tile * 16 + 16 > valid;
 #pragma unroll
     for (int j = 0; j < kVLoads; ++j) {
       const u32x4 z = {0u, 0u, 0u, 0u};
@@ -350,7 +360,7 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
       *reinterpret_cast<BT_LDS u32x4*>((BT_LDS unsigned char*)vtile + j * 1024 + lane * 16) = dead ? z : vr[j];
     }
     if (more) {
-      if (it == 0) issue_k(tile + tstride);
+      if (first) issue_k(tile + tstride);
       issue_v(tile + tstride);
     }
 
@@ -384,7 +394,7 @@ __global__ __launch_bounds__(W * 64, 1) void gqa_decode_split_kernel(DecodeSplit
     // O is zero before the first tile, where alpha is always 0 (m_run starts
     // at -inf): no rescale there (C2 1k / 4k / 32k -0.15 / -0.15 / -0.09 us
     // together with the folded mirror adds below, bit-identical).
-    if (it > 0 && __builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+    if (!first && __builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
       for (int i = 0; i < kDTiles; ++i) oacc[i] *= alpha;
     }
