@@ -160,6 +160,11 @@ struct OpFAdd {
 struct OpFMaxf {
   __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b))); }
 };
+// NaN-propagating maximum (v_maximum_f32): unlike fmaxf it needs no operand
+// canonicalisation, so a butterfly of it is one lane move and one max.
+struct OpFMax {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return __float_as_uint(fmax_nc(__uint_as_float(a), __uint_as_float(b))); }
+};
 struct OpUMax {
   __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
 };
@@ -187,6 +192,7 @@ __device__ __forceinline__ uint32_t wave_op_desc(uint32_t x, Op op) {
 }
 __device__ __forceinline__ float wave_sum(float x) { return __uint_as_float(wave_op_desc(__float_as_uint(x), OpFAdd{})); }
 __device__ __forceinline__ float wave_fmaxf(float x) { return __uint_as_float(wave_op_desc(__float_as_uint(x), OpFMaxf{})); }
+__device__ __forceinline__ float wave_max(float x) { return __uint_as_float(wave_op_desc(__float_as_uint(x), OpFMax{})); }
 __device__ __forceinline__ uint32_t wave_umax(uint32_t x) { return wave_op_desc(x, OpUMax{}); }
 // Sum over the lane bits at and above log2(FROM), masks FROM, 2 FROM, ..., 32.
 template <int FROM>
