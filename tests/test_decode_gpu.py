@@ -194,7 +194,10 @@ def test_one_kv_head_at_16k_uses_256_splits(hip_backend):
 
 
 @pytest.mark.parametrize("heads,kv,dim", [(8, 2, 128), (8, 2, 64), (4, 4, 256), (8, 1, 256),
-                                          (16, 2, 128), (6, 2, 256), (12, 2, 64), (2, 1, 256)])
+                                          (16, 2, 128), (6, 2, 256), (12, 2, 64), (2, 1, 256),
+                                          # kv head counts that are not powers of two (the grid
+                                          # index is then split by a division, not a shift)
+                                          (6, 3, 256), (24, 6, 128), (5, 5, 64)])
 def test_other_served_shapes(hip_backend, heads, kv, dim):
     case = wl.decode_inputs(25, heads, kv, dim, 3000, 2345)
     ref = orc.fixed_decode(case.q.float(), case.k.float(), case.v.float(), case.pos, case.scale)

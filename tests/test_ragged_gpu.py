@@ -41,6 +41,13 @@ def test_ragged_any_split_plan(hip_backend, target):
     _check(_run(hip_backend, case, target), case)
 
 
+def test_ragged_three_kv_heads(hip_backend):
+    # A kv head count that is not a power of two: the kernel splits the
+    # work-group index by a division instead of a shift.
+    case = wl.c5_inputs(lens=[1, 33, 500, 4097, 64], heads=6, kv_heads=3, dim=128)
+    _check(_run(hip_backend, case), case)
+
+
 def _host_plan_tables(lens, target):
     import ctypes
 
