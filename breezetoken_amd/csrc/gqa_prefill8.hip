@@ -419,18 +419,25 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     // The V^T block's power-of-two scale enters P' = P * 2^shift through the
     // exp2 bias; the row sum takes P.
     auto softmax = [&](floatx4 (&sacc)[4], u32x4 (&out)[2], int ek, int eb) -> float {
-      float tmax = -INFINITY;
+      float lmax = -INFINITY;
   #pragma unroll
       for (int sub = 0; sub < 4; ++sub)
   #pragma unroll
-        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[sub][r]);
+        for (int r = 0; r < 4; ++r) lmax = fmaxf(lmax, sacc[sub][r]);
       const float c_log2 = __builtin_ldexpf(c_col, ek);  // with the K block's scale
-      tmax = xor_fmaxf<16>(tmax);
-      tmax = halves_max(tmax) * c_log2;
-      const bool move = tmax > m_ref + kLazy8;
-      const float m_new = move ? tmax : m_ref;
-      const float alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
-      m_ref = m_new;
+      // The column's max is one of its lane groups' own maxes (or NaN), so it
+      // passes the lazy bound exactly when one group's does (scaling by
+      // c_log2 > 0 keeps the order): the cross-lane reduction runs only when
+      // some column's reference max may move, rare after a row's first keys.
+      float alpha = 1.f;
+      if (__builtin_amdgcn_ballot_w64(lmax * c_log2 > m_ref + kLazy8)) {
+        float tmax = xor_fmaxf<16>(lmax);
+        tmax = halves_max(tmax) * c_log2;
+        const bool move = tmax > m_ref + kLazy8;
+        const float m_new = move ? tmax : m_ref;
+        alpha = move ? fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref is -inf
+        m_ref = m_new;
+      }
       const int e_new = vexp_next(e_run, eb);
       const int shift = vexp_shift(e_new, eb);
       const float neg_m = (m_ref == -INFINITY ? 0.f : -m_ref) + (float)shift;

@@ -334,15 +334,22 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   // scale exponent changes from e_old to e_new, P^T into pk[t].
   auto softmax_tile = [&](int t, const float (&s)[8], int ek, int shift, int e_old, int e_new) {
     const float c_log2 = __builtin_ldexpf(c_col[t], ek);  // log2-domain factor of the scaled scores
-    float tmax = fmax_nc(fmax_nc(fmax_nc(s[0], s[1]), fmax_nc(s[2], s[3])),
-                         fmax_nc(fmax_nc(s[4], s[5]), fmax_nc(s[6], s[7])));
-    tmax = rows16_max(tmax);
-    tmax = halves_max(tmax) * c_log2;
-    const bool move = tmax > m_ref[t] + kLazyP;
-    const float m_new = move ? tmax : m_ref[t];
-    float alpha = move ? fast_exp2(m_ref[t] - m_new) : 1.f;  // 0 when m_ref is -inf
-    m_ref[t] = m_new;
-    const float bias = (m_new == -INFINITY ? 0.f : -m_new) + (float)shift;
+    const float lmax = fmax_nc(fmax_nc(fmax_nc(s[0], s[1]), fmax_nc(s[2], s[3])),
+                               fmax_nc(fmax_nc(s[4], s[5]), fmax_nc(s[6], s[7])));
+    // The column's max over its four lane groups passes the lazy bound exactly
+    // when one group's own max does (scaling by c_log2 > 0 keeps the order),
+    // so the cross-lane reduction runs only when some column's reference max
+    // may move: rare after a row's first keys.
+    float alpha = 1.f;
+    if (__builtin_amdgcn_ballot_w64(lmax * c_log2 > m_ref[t] + kLazyP)) {
+      float tmax = rows16_max(lmax);
+      tmax = halves_max(tmax) * c_log2;
+      const bool move = tmax > m_ref[t] + kLazyP;
+      const float m_new = move ? tmax : m_ref[t];
+      alpha = move ? fast_exp2(m_ref[t] - m_new) : 1.f;  // 0 when m_ref is -inf
+      m_ref[t] = m_new;
+    }
+    const float bias = (m_ref[t] == -INFINITY ? 0.f : -m_ref[t]) + (float)shift;
     float e[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) e[r] = fast_exp2(fmaf(s[r], c_log2, bias));
