@@ -467,15 +467,25 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     };
     const int kb_diag = (P0 + q0 + 1) / kKB8;  // earlier blocks need no mask
 
+    // The first d-step's K fragments of each block are read before the
+    // barrier that ends the block before it (the barrier in that block's
+    // middle published them), so they arrive while the waves meet there; the
+    // barrier leaves them in flight: every other LDS read of the block is
+    // consumed by its MFMAs, and the K buffer they come from is refilled only
+    // after the next block's Q.K^T.  They are read even when no block follows
+    // (a stale buffer's values go unused), so f0 is always written and the
+    // compiler keeps no older copy of it alive.
+    auto end_block = [&](auto b_next, u32x4 (&f0)[4]) {
+      k_first(b_next, f0);
+      asm volatile("s_barrier" ::: "memory");
+    };
+    u32x4 f0[4];
     wait_all();
     __syncthreads();
     {
       floatx4 sacc[4];
-      {
-        u32x4 f0[4];
-        k_first(Buf8<0>{}, f0);
-        qk(Buf8<0>{}, sacc, f0);
-      }
+      k_first(Buf8<0>{}, f0);
+      qk(Buf8<0>{}, sacc, f0);
       barrier();
       if (kb0 + 2 <= last) copy_k(Buf8<0>{}, kb0 + 2);
       if (kb0 >= kb_diag) mask(kb0, sacc);
@@ -484,15 +494,13 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       softmax(sacc, pk, ek_c, eb_c);  // O is still zero: its factor does not matter
       ek_c = ek_n;
       eb_c = eb_n;
-      barrier();
+      end_block(Buf8<1>{}, f0);  // K_{kb0+1} arrived with the prologue's copies
     }
     // Block kb: A: S_kb = K_kb . Q^T; B: O += V_{kb-1} . P_{kb-1} beside the
     // softmax of S_kb.
     auto step = [&](auto b, int kb) {
       constexpr int B = decltype(b)::value;
       const bool second = kb == kb0 + 1;  // its V^T went out in the prologue
-      u32x4 f0[4];
-      k_first(b, f0);
       if (!second) copy_v(b, kb);
       int ek_n, eb_n;
       floatx4 sacc[4];
@@ -501,9 +509,9 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       // share the LDS reads' counter and return out of order, so issued
       // earlier they would hold the first MFMA until they arrive.
       scales(kb + 1, ek_n, eb_n);
-      // V_{kb-1}; issued after it: K_{kb+1} (if any) and V_kb (in the second
-      // block: V_{kb0+1}, from the prologue).
-      wait_tiles((kb + 1 <= last ? 1 : 0) + 1);
+      // V_{kb-1} and K_{kb+1} (if any); issued after them: V_kb (except in the
+      // second block, whose V^T went out in the prologue).
+      wait_tiles(second ? 0 : 1);
       barrier();
       if (kb + 2 <= last) copy_k(b, kb + 2);
       if (kb >= kb_diag) mask(kb, sacc);
@@ -515,10 +523,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       rescale(alpha);
       pk[0] = pk_next[0];
       pk[1] = pk_next[1];
-      // K_{kb+1} (if any); issued after it: V_kb (except in the second block,
-      // whose V^T went out in the prologue) and K_{kb+2} (if any).
-      wait_tiles((second ? 0 : 1) + (kb + 2 <= last ? 1 : 0));
-      barrier();
+      end_block(Buf8<B ^ 1>{}, f0);
     };
     // Every pass of the loop ends with a buffer-0 step, so no path reaches the
     // loop head with a copy into buffer 1 in flight (the compiler would have to
