@@ -559,9 +559,12 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       // wave waits at the next barrier, which leaves them in flight: the P.V
       // reads before them are consumed by its MFMAs, and K of st is
       // overwritten only after this step's Q.K^T.  C4 S = 8192 in one process:
-      // 267.1 -> 263.5 us (bf16 q), 393.9 -> 387.8 us (f32 q), bit-identical;
-      // the same for A (its K then waited for one phase after its copy is
-      // issued) gained nothing more.
+      // 267.1 -> 263.5 us (bf16 q), 393.9 -> 387.8 us (f32 q), bit-identical.
+      // The same for A gained nothing more, with its K waited for one phase
+      // after its copy is issued or with its K copies moved a phase earlier
+      // (A's tile-copy issue after its barrier already covers the first
+      // reads); B's first V^T fragments read the same way at the end of its
+      // Q.K^T phase cost 1.4% with f32 q.
       if (w0) k_first(Kc, kf);
       asm volatile("s_barrier" ::: "memory");
       if (w1) copy_v(Vn, st + 1);
