@@ -15,11 +15,12 @@
 //    per step (all heads of a GQA group read the same K/V);
 //  * a work-group holds two groups, A and B, and the query blocks j and
 //    N-1-j of one kv head: together they need N+1 steps whatever j is, so
-//    every work-group does the same work.  A runs block j, then the first
-//    keys of block N-1-j; B runs the remaining keys of block N-1-j; both take
+//    every work-group does the same work.  A runs block j, then the last
+//    keys of block N-1-j; B runs the other keys of block N-1-j; both take
 //    ceil((N+1)/2) steps in lockstep (two barrier phases per step: one group
 //    runs Q.K^T + softmax while the other runs P.V), and the two halves of
-//    block N-1-j are merged through LDS at the end;
+//    block N-1-j are merged through LDS at the end.  While A runs block j the
+//    two groups read the same key units, and A reads B's tiles;
 //  * Q.K^T runs on fp16 MFMAs: q (f32, as the reference keeps it through
 //    prefill.py:49-68, or bf16) is rounded to fp16 after scaling each query
 //    row by a power of two, and K comes from the pre-pass's fp16 image, scaled
@@ -85,7 +86,7 @@ __host__ __device__ inline PairShape pair_shape(int group, int nqt) {
 }
 
 // One group's share of a pair work-group.  GRP 0 (A) runs query block qa's
-// keys, then the first keys of qb; GRP 1 (B) the rest of qb.  K0/K1/V0/V1 are
+// keys, then the last keys of qb; GRP 1 (B) the rest of qb.  K0/K1/V0/V1 are
 // this group's double-buffered tiles (distinct LDS objects, so the compiler
 // can tell a copy into one buffer from a read of another); xbuf(i) is tile
 // buffer i of the eight, reused for the final merge.
@@ -99,6 +100,7 @@ struct Sel {
 template <int D, int NQT, bool LO, int GRP, typename XB>
 __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char* K0, unsigned char* K1,
                                            unsigned char* V0, unsigned char* V1, XB xbuf, float* xs) {
+  auto xbuf_c = [&](int i) { return reinterpret_cast<unsigned char*>(xbuf(i)); };
   constexpr int kDSteps = D / 32;
   constexpr int kDTiles = D / 16;
   constexpr int kRowBytes = D * 2;
@@ -122,23 +124,30 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   const int na = qa != qb ? n_units(qa) : 0;
   const int nb = n_units(qb);
   // A runs block qa's na units, then the last xa units of block qb; B runs
-  // qb's first nb - xa units.  So both groups of every work-group read key
-  // unit s at step s for most of the kernel, and the work-groups on an XCD
-  // share each K/V tile through L2.  When na is odd A starts one step late,
-  // so its switch to block qb falls on an even step; the step count is even
-  // too.  Then the key loop is unrolled by two with a constant buffer per
-  // step and no branch between its copies.
+  // qb's first nb - xa units.  Both groups read key unit s - lead at step s
+  // until A's switch to block qb (the units block qa needs are the first
+  // units of block qb too): there A reads B's K and V^T tiles and copies none
+  // of its own, and the work-groups on an XCD share each tile through L2.
+  // When na is odd both groups start one step late, so A's switch falls on an
+  // even step; the step count is even too.  Then the key loop is unrolled by
+  // two with a constant buffer per step and no branch between its copies.
+  // C4 S = 8192 / 12000 in one process, against A copying every tile: 264.1
+  // -> 260.9 / 669.9 -> 645.2 us (bf16 q), 398.0 -> 387.3 us (f32 q).  A
+  // work-group whose qa is small shares few steps and gains little, so the
+  // gain shows where work-groups outnumber the CUs and others take their
+  // place.
   const int lead = na & 1;
-  const int xa = max(0, (nb - na - lead) / 2);
-  const int steps_a = lead + na + xa;
-  const int steps_b = nb - xa;
+  const int sw = lead + na;                        // A's first step on block qb (even)
+  const int xa = max(0, (nb - na) / 2);
+  const int steps_a = sw + xa;
+  const int steps_b = lead + nb - xa;
   const int n_steps = (max(steps_a, steps_b) + 1) & ~1;
   const int my_steps = GRP == 0 ? steps_a : steps_b;
-  const int first = GRP == 0 ? lead : 0;          // this group's first working step
-  const int sw = lead + na;                        // A's first step on block qb (even)
-  // Unit of step s: (query block, key unit).
+  const int first = lead;                          // both groups' first working step
+  // Unit of step s: (query block, key unit); shared(s): A reads B's tiles.
   auto unit_blk = [&](int st) { return (GRP == 0 && st < sw) ? qa : qb; };
-  auto unit_key = [&](int st) { return GRP == 0 ? (st < sw ? st - lead : nb - xa + st - sw) : st; };
+  auto unit_key = [&](int st) { return GRP == 0 ? (st < sw ? st - lead : nb - xa + st - sw) : st - lead; };
+  auto shared = [&](int st) { return st >= lead && st < sw; };
 
   const int nblk64 = (nkeys + kPrefillKeyBlock - 1) / kPrefillKeyBlock;
   const uint32_t img_bytes = (uint32_t)nblk64 * kPrefillKeyBlock * kRowBytes;
@@ -504,7 +513,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   };
 
   // The first tiles go out before the q loads, so the two latencies overlap.
-  if (first < my_steps) {
+  if (first < my_steps && !(GRP == 0 && shared(first))) {
     if (first & 1) { copy_k(K1, first); copy_v(V1, first); } else { copy_k(K0, first); copy_v(V0, first); }
   }
   int cur_blk = unit_blk(first);
@@ -517,11 +526,13 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
   //   A: | K_st ready  S = Q.K^T, softmax      | V_st ready  O += P.V       |
   //   B: | V_st-1 ready  O += P_{st-1}.V_{st-1} | K_st ready  S = Q.K^T, softmax |
   // Copies go out as soon as their buffer is free: A requests K and V^T of
-  // step st + 1 at the first barrier of st; B requests K of st + 1 at the first
-  // barrier and V^T of st + 1 at the second (after its P.V of st - 1), and
-  // reads its first K fragments of st before the second.
-  auto step = [&](auto bufsel, int st, int& eb, int& ek) {
+  // step st + 1 at the first barrier of st (after its switch: before it, it
+  // reads B's); B requests K of st + 1 at the first barrier and V^T of st + 1
+  // at the second (after its P.V of st - 1), and reads its first K fragments
+  // of st before the second.
+  auto step = [&](auto bufsel, auto shtag, int st, int& eb, int& ek) {
     constexpr bool kOdd = decltype(bufsel)::value;
+    constexpr bool kShared = decltype(shtag)::value;  // A's steps before its switch
     unsigned char* Kc = kOdd ? K1 : K0;   // this step's buffers
     unsigned char* Vc = kOdd ? V1 : V0;
     unsigned char* Kn = kOdd ? K0 : K1;   // the next step's (and the previous step's)
@@ -530,7 +541,24 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     // The wave running Q.K^T + softmax gets issue priority, so its MFMAs go
     // first and its softmax overlaps the other wave's P.V.
     u32x4 kf[kKLead + 1][2];
-    if constexpr (GRP == 0) {
+    if constexpr (GRP == 0 && kShared) {
+      // B's tiles of this step: B waits for their copies before the
+      // barriers that start A's two phases.
+      unsigned char* Kb = kOdd ? xbuf_c(5) : xbuf_c(4);
+      unsigned char* Vb = kOdd ? xbuf_c(7) : xbuf_c(6);
+      barrier();
+      if (w0) k_first(Kb, kf);
+      int eb_n, ek_n;
+      if (w1 && !shared(st + 1)) { copy_k(Kn, st + 1); copy_v(Vn, st + 1); }  // A's first own tiles
+      __builtin_amdgcn_s_setprio(1);
+      if (w0) qk_sm(Kb, st, eb, ek, kf, [&] { unit_scales(st + 1, eb_n, ek_n); });
+      else unit_scales(st + 1, eb_n, ek_n);
+      __builtin_amdgcn_s_setprio(0);
+      eb = eb_n;
+      ek = ek_n;
+      barrier();
+      if (w0) pv(Vb);
+    } else if constexpr (GRP == 0) {
       wait_tiles(1);  // K of st (its V^T was issued after it)
       barrier();
       if (w0) k_first(Kc, kf);
@@ -566,6 +594,9 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       // reads); B's first V^T fragments read the same way at the end of its
       // Q.K^T phase cost 1.4% with f32 q.
       if (w0) k_first(Kc, kf);
+      // In a shared step A reads V^T of st in the phase that starts here (one
+      // phase before B does).
+      if (shared(st) && w0) wait_tiles(w1 ? 1 : 0);  // V^T of st (behind it: K of st + 1)
       asm volatile("s_barrier" ::: "memory");
       if (w1) copy_v(Vn, st + 1);
       __builtin_amdgcn_s_setprio(1);
@@ -576,18 +607,18 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       ek = ek_n;
     }
   };
-  auto run = [&](int s0, int s1) {  // s0 and s1 even
+  auto run = [&](auto shtag, int s0, int s1) {  // s0 and s1 even
     int eb, ek;
     unit_scales(s0, eb, ek);
     for (int st = s0; st < s1; st += 2) {
-      step(Sel<false>{}, st, eb, ek);
-      step(Sel<true>{}, st + 1, eb, ek);
+      step(Sel<false>{}, shtag, st, eb, ek);
+      step(Sel<true>{}, shtag, st + 1, eb, ek);
     }
   };
   if constexpr (GRP == 0) {
     // Block qa, then (after storing it) the first keys of block qb.
     const int s_switch = min(sw, n_steps);
-    run(0, s_switch);
+    run(Sel<true>{}, 0, s_switch);
     if (na > 0 && s_switch < my_steps) {
       float lsum[NQT];
       row_sums(lsum);
@@ -597,9 +628,9 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       load_q(qb);
       reset();
     }
-    run(s_switch, n_steps);
+    run(Sel<false>{}, s_switch, n_steps);
   } else {
-    run(0, n_steps);
+    run(Sel<false>{}, 0, n_steps);
   }
 
   // B's P.V of its last step (both groups pass the barrier that publishes it).
