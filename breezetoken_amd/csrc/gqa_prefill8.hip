@@ -767,7 +767,24 @@ hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t str
   const int ys = p.kv_heads * p.head_subs;  // grid y: (kv head, head subset)
   const dim3 grid = paired ? dim3(((nqb + 1) / 2) * p.pair_parts, ys, 1)
                            : dim3(nqb, ys, p.kb_chunk > 0 ? p.max_chunks : 1);
-  const dim3 cgrid(nqb, ys, kRows8 * head_dim / 4 / 256);
+  // The combine's work-groups run the query blocks heaviest first; under the
+  // uniform split only the heaviest ones have more than one chunk (a query
+  // block's key blocks grow with its index), so its grid stops there -- at a
+  // multiple of 8 work-groups in x, which keeps each query block's merge on
+  // the XCD (work-group id mod 8) whose L2 holds its partials when nqb is a
+  // multiple of 8: C4 S = 2048 50.5 -> 48.5 us per call; S = 512 with 12 of
+  // its 16 columns took 22.8 against 21.7 us.
+  int cx = nqb;
+  if (p.kb_chunk > 0) {
+    cx = 0;
+    for (int qb = nqb - 1; qb >= 0; --qb) {
+      const int nkb = (p.q_offset + min(p.seqlen, (qb + 1) * pos_per_wg) + kKB8 - 1) / kKB8;
+      if (nkb <= p.kb_chunk) break;
+      ++cx;
+    }
+    cx = min(nqb, (cx + 7) & ~7);
+  }
+  const dim3 cgrid(cx, ys, kRows8 * head_dim / 4 / 256);
   // Work-groups with at most two key blocks each convert them themselves,
   // unless the caller keeps the images for later chunks.
   const int longest = (p.q_offset + p.seqlen + kKB8 - 1) / kKB8;
@@ -782,7 +799,7 @@ hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t str
     if (paired) hipLaunchKernelGGL((gqa_prefill8_kernel<Dk, false, true, LOk>), grid, dim3(kWaves8 * 64), 0, stream, p);
     else if (direct) hipLaunchKernelGGL((gqa_prefill8_kernel<Dk, true, false, LOk>), grid, dim3(kWaves8 * 64), 0, stream, p);
     else hipLaunchKernelGGL((gqa_prefill8_kernel<Dk, false, false, LOk>), grid, dim3(kWaves8 * 64), 0, stream, p);
-    if (split) hipLaunchKernelGGL(prefill_combine_kernel<Dk>, cgrid, dim3(256), 0, stream, p);
+    if (split && cx > 0) hipLaunchKernelGGL(prefill_combine_kernel<Dk>, cgrid, dim3(256), 0, stream, p);
   };
   // f32 q takes the two-term (hi + lo) Q.K^T; bf16 q converts to fp16 exactly.
   switch (head_dim) {
