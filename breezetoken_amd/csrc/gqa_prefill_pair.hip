@@ -616,7 +616,7 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     }
   };
   if constexpr (GRP == 0) {
-    // Block qa, then (after storing it) the first keys of block qb.
+    // Block qa (on B's tiles), then (after storing it) the last keys of block qb.
     const int s_switch = min(sw, n_steps);
     run(Sel<true>{}, 0, s_switch);
     if (na > 0 && s_switch < my_steps) {
