@@ -542,36 +542,65 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     // ---- epilogue: row sums over the four lane groups, normalise, store -------
     l_run = xor_sum<16>(l_run);
     l_run = halves_sum(l_run);
+    const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
+    // Rows leave through LDS, so that every store writes whole 16-byte slices
+    // of rows (a wave's store covers 2 rows of bf16 at D = 256) instead of 8-
+    // or 16-byte pieces of 16 rows: at config 4, S = 128 took 13.5 against
+    // 16.0 us per call.  Wave w stages 16 rows of 2D bytes (bf16 rows, or
+    // f32 rows in two column halves) in quarter w % 4 of K buffer w / 4 --
+    // every wave is past its last Q.K^T and the barrier after the loop --
+    // with 16-byte chunk c of row r in slot c ^ r.
+    unsigned char* stage = (wave < 4 ? k_lds0 : k_lds1) + (wave & 3) * (kQ8 * D * 2);
+    constexpr int kChunks = D / 8;          // 16-byte chunks of a staged row
+    constexpr int kRowsPer = 64 / kChunks;  // staged rows per store
+    // Store the staged rows: row r to dst(r) + col_bytes (dst(r) null: skipped).
+    auto drain = [&](auto&& dst, int col_bytes) {
+  #pragma unroll
+      for (int j = 0; j < kQ8 / kRowsPer; ++j) {
+        const int r = j * kRowsPer + lane / kChunks, c = lane % kChunks;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(stage + r * (D * 2) + (c ^ r) * 16);
+        if (unsigned char* d = dst(r)) *reinterpret_cast<u32x4*>(d + col_bytes + c * 16) = x;
+      }
+    };
+    // f32 rows in two halves of D / 2 columns (d tiles [h * kDTiles / 2, +kDTiles / 2)).
+    auto store_f32 = [&](auto&& dst) {
+  #pragma unroll
+      for (int h = 0; h < 2; ++h) {
+  #pragma unroll
+        for (int dt = h * kDTiles / 2; dt < (h + 1) * kDTiles / 2; ++dt) {
+          const int c = (dt - h * kDTiles / 2) * 4 + g4;  // chunk of columns dt*16 + g4*4 ..
+          *reinterpret_cast<float4*>(stage + i16 * (D * 2) + (c ^ i16) * 16) =
+              float4{oacc[dt][0] * inv, oacc[dt][1] * inv, oacc[dt][2] * inv, oacc[dt][3] * inv};
+        }
+        drain(dst, h * (D * 2));
+      }
+    };
     if (nchunks > 1) {
       // One chunk of a split query block: normalised partial and LSE of row
-      // (wave, query column) for prefill_combine_kernel.
+      // (wave, query column) for prefill_combine_kernel; the wave's 16 rows
+      // are contiguous.
       const int64_t slot = ((int64_t)ysub * nqb + qblk) * p.max_chunks + chunk;
-      const int row = wave * kQ8 + i16;
-      float* prow = p.part + (slot * kRows8 + row) * D;
-      const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
-  #pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) {
-        const int d = dt * 16 + g4 * 4;
-        *reinterpret_cast<float4*>(prow + d) =
-            float4{oacc[dt][0] * inv, oacc[dt][1] * inv, oacc[dt][2] * inv, oacc[dt][3] * inv};
-      }
-      if (g4 == 0) p.lse[slot * kRows8 + row] = l_run > 0.f ? fast_log2(l_run) + m_ref : -INFINITY;
+      unsigned char* prows = reinterpret_cast<unsigned char*>(p.part + (slot * kRows8 + wave * kQ8) * D);
+      store_f32([&](int r) -> unsigned char* { return prows + r * (D * 4); });
+      if (g4 == 0) p.lse[slot * kRows8 + wave * kQ8 + i16] = l_run > 0.f ? fast_log2(l_run) + m_ref : -INFINITY;
       return;
     }
-    if (q0 < S && my_q < S) {
-      const float inv = l_run > 0.f ? __builtin_ldexpf(1.f / l_run, e_run) : 0.f;
-      const int64_t orow = (int64_t)my_q * p.out_stride_tok + (int64_t)head * p.out_stride_head;
+    auto out_row = [&](int r) -> unsigned char* {
+      if (q0 + r >= S) return nullptr;
+      const int64_t e = (int64_t)(q0 + r) * p.out_stride_tok + (int64_t)head * p.out_stride_head;
+      return reinterpret_cast<unsigned char*>(p.out) + e * (p.out_bf16 ? 2 : 4);
+    };
+    if (p.out_bf16) {
   #pragma unroll
       for (int dt = 0; dt < kDTiles; ++dt) {
-        const int d = dt * 16 + g4 * 4;
-        const float o0 = oacc[dt][0] * inv, o1 = oacc[dt][1] * inv, o2 = oacc[dt][2] * inv, o3 = oacc[dt][3] * inv;
-        if (p.out_bf16) {
-          const u32x2 pk2 = {f32x2_to_bf16x2_bits(o0, o1), f32x2_to_bf16x2_bits(o2, o3)};
-          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + orow + d) = pk2;
-        } else {
-          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + d) = float4{o0, o1, o2, o3};
-        }
+        const u32x2 pk2 = {f32x2_to_bf16x2_bits(oacc[dt][0] * inv, oacc[dt][1] * inv),
+                           f32x2_to_bf16x2_bits(oacc[dt][2] * inv, oacc[dt][3] * inv)};
+        const int c = dt * 2 + (g4 >> 1);  // chunk of columns dt*16 + g4*4 ..
+        *reinterpret_cast<u32x2*>(stage + i16 * (D * 2) + (c ^ i16) * 16 + (g4 & 1) * 8) = pk2;
       }
+      drain(out_row, 0);
+    } else {
+      store_f32(out_row);
     }
   };
   auto n_blocks = [&](int qb) { return (P0 + min(S, (qb + 1) * pos_per_wg) + kKB8 - 1) / kKB8; };
