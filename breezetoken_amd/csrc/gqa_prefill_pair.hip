@@ -301,6 +301,53 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       }
     }
   };
+  // The same through LDS, so that every store writes whole 16-byte slices of
+  // rows instead of 8- or 16-byte pieces of 16 rows: q-tile t's 16 rows (2D
+  // bytes each: bf16 rows, or f32 rows in two column halves) go to stage(t),
+  // this wave's own 16 x 2D bytes, with 16-byte chunk c of row r in slot
+  // c ^ r, and are read back a row slice per lane.
+  auto store_staged = [&](int blk, const float (&lsum)[NQT], auto&& stage) {
+    constexpr int kChunks = D / 8;          // 16-byte chunks of a staged row
+    constexpr int kRowsPer = 64 / kChunks;  // staged rows per store
+#pragma unroll
+    for (int t = 0; t < NQT; ++t) {
+      unsigned char* st_ = stage(t);
+      const int row0 = blk * sh.pos + poff[t];
+      const float inv = lsum[t] > 0.f ? __builtin_ldexpf(1.f / lsum[t], e_run) : 0.f;
+      unsigned char* obase = reinterpret_cast<unsigned char*>(p.out) +
+                             (int64_t)head[t] * p.out_stride_head * (p.out_bf16 ? 2 : 4);
+      const int64_t row_bytes = p.out_stride_tok * (p.out_bf16 ? 2 : 4);
+      auto drain = [&](int col_bytes) {
+#pragma unroll
+        for (int j = 0; j < 16 / kRowsPer; ++j) {
+          const int r = j * kRowsPer + lane / kChunks, c = lane % kChunks;
+          const u32x4 x = *reinterpret_cast<const u32x4*>(st_ + r * (D * 2) + (c ^ r) * 16);
+          if (row0 + r < S) *reinterpret_cast<u32x4*>(obase + (row0 + r) * row_bytes + col_bytes + c * 16) = x;
+        }
+      };
+      if (p.out_bf16) {
+#pragma unroll
+        for (int dt = 0; dt < kDTiles; ++dt) {
+          const u32x2 pk2 = {f32x2_to_bf16x2_bits(oacc[t][dt][0] * inv, oacc[t][dt][1] * inv),
+                             f32x2_to_bf16x2_bits(oacc[t][dt][2] * inv, oacc[t][dt][3] * inv)};
+          const int c = dt * 2 + (g4 >> 1);  // chunk of columns dt*16 + g4*4 ..
+          *reinterpret_cast<u32x2*>(st_ + i16 * (D * 2) + (c ^ i16) * 16 + (g4 & 1) * 8) = pk2;
+        }
+        drain(0);
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int dt = h * kDTiles / 2; dt < (h + 1) * kDTiles / 2; ++dt) {
+            const int c = (dt - h * kDTiles / 2) * 4 + g4;
+            *reinterpret_cast<float4*>(st_ + i16 * (D * 2) + (c ^ i16) * 16) =
+                float4{oacc[t][dt][0] * inv, oacc[t][dt][1] * inv, oacc[t][dt][2] * inv, oacc[t][dt][3] * inv};
+          }
+          drain(h * (D * 2));
+        }
+      }
+    }
+  };
   auto row_sums = [&](float (&lsum)[NQT]) {
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
@@ -622,7 +669,12 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
     if (na > 0 && s_switch < my_steps) {
       float lsum[NQT];
       row_sums(lsum);
-      store(cur_blk, lsum);
+      // A's K and V buffers 1 are free here: before the switch A reads B's
+      // tiles (and its own buffers 0 in a lead step); the first copies into
+      // buffers 1 come after the barrier that opens step s_switch.
+      store_staged(cur_blk, lsum, [&](int) -> unsigned char* {
+        return reinterpret_cast<unsigned char*>(gw < 2 ? xbuf(1) : xbuf(3)) + (gw & 1) * (16 * D * 2);
+      });
       asm volatile("" ::: "memory");  // the next block's q loads stay behind these stores
       cur_blk = qb;
       load_q(qb);
@@ -689,7 +741,8 @@ __device__ __forceinline__ void pair_group(const PrefillParams& p, unsigned char
       lsum[t] = la * wa + lsum[t] * wb;
     }
     e_run = e_m;
-    store(qb, lsum);
+    // Each wave stages q-tile t in the buffer it just read A's partial from.
+    store_staged(qb, lsum, [&](int t) -> unsigned char* { return reinterpret_cast<unsigned char*>(xbuf(gw * NQT + t)); });
   }
 }
 
