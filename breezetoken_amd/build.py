@@ -19,6 +19,10 @@ LIB = PKG / "libbreezetoken_amd.so"
 # Machine-floor probes for bench.py --mode floor (not part of the attention ABI).
 PROBE_SRC = PKG / "probes" / "floor.hip"
 PROBE_LIB = PKG / "libbt_floor.so"
+# The product library with gqa_prefill8.hip built under BT_TIMELINE: the
+# prefill timeline probe (probes/timeline.py) loads it in place of LIB.
+TIMELINE_SRC = CSRC / "gqa_prefill8.hip"
+TIMELINE_LIB = PKG / "libbt_timeline.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -41,8 +45,8 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; install ROCm or set HIPCC")
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, extra: tuple[str, ...] = ()) -> None:
+    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
@@ -69,13 +73,16 @@ def build(verbose: bool = True) -> Path:
     objdir.mkdir(exist_ok=True)
     objs = [objdir / (s.stem + ".o") for s in srcs]
     probe_obj = objdir / "floor_probe.o"
-    jobs = list(zip(srcs, objs)) + [(PROBE_SRC, probe_obj)]
+    tl_obj = objdir / "prefill8_timeline.o"
+    jobs = [(s, o, ()) for s, o in zip(srcs, objs)]
+    jobs += [(PROBE_SRC, probe_obj, ()), (TIMELINE_SRC, tl_obj, ("-DBT_TIMELINE",))]
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
-        list(ex.map(lambda so: _compile(*so), jobs))
+        list(ex.map(lambda job: _compile(*job), jobs))
     _link(objs, LIB)
     _link([probe_obj], PROBE_LIB)
+    _link([o for o in objs if o.stem != TIMELINE_SRC.stem] + [tl_obj], TIMELINE_LIB)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources, and {PROBE_LIB.name}", file=sys.stderr)
+        print(f"built {LIB} from {len(srcs)} sources, {PROBE_LIB.name} and {TIMELINE_LIB.name}", file=sys.stderr)
     return LIB
 
 

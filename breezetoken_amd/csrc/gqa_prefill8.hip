@@ -108,6 +108,32 @@ __host__ __device__ inline int pair_chunks(int qb, int nqb, int parts, NB n_bloc
 
 }  // namespace
 
+// Timeline build only (-DBT_TIMELINE, libbt_timeline.so; never the product
+// library): waves 0 and 4 of each of the first kTimelineWGs work-groups
+// record s_memrealtime (the device's 100 MHz clock) at eight points of a
+// segment -- start, q in registers, first tiles published, first block done,
+// key loop done, last P.V issued, stores issued, stores complete -- into
+// bt_tl_buf[(work-group * 2 + (wave == 4)) * 8 + point], with vector stores
+// after the segment's own.  A work-group with two segments keeps the second's.
+#ifdef BT_TIMELINE
+constexpr int kTimelineWGs = 4096;
+constexpr int kTimelineSlots = kTimelineWGs * 16;
+__device__ unsigned long long bt_tl_buf[kTimelineSlots];
+#define BT_TL(k) (tl[k] = __builtin_amdgcn_s_memrealtime())
+#define BT_TL_END()                                                                                   \
+  do {                                                                                                \
+    tl[6] = __builtin_amdgcn_s_memrealtime();                                                         \
+    __builtin_amdgcn_s_waitcnt(0x0f70); /* vmcnt(0): the stores are complete */                     \
+    tl[7] = __builtin_amdgcn_s_memrealtime();                                                         \
+    const int wg_ = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));            \
+    if (lane == 0 && (wave == 0 || wave == 4) && wg_ < kTimelineWGs)                                  \
+      for (int k_ = 0; k_ < 8; ++k_) bt_tl_buf[(wg_ * 2 + (wave == 4)) * 8 + k_] = tl[k_];            \
+  } while (0)
+#else
+#define BT_TL(k) ((void)0)
+#define BT_TL_END() ((void)0)
+#endif
+
 // DIRECT: a work-group with at most two key blocks converts them from the bf16
 // cache straight into its LDS tiles (the layout and rounding of the images
 // of gqa_prefill_vt.hip, same block scales), so a short prompt needs no
@@ -154,6 +180,10 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   // One segment: key blocks [kb0, kb1) of query block qblk, chunk `chunk` of
   // its nchunks (nchunks > 1: the segment writes a partial for the combine).
   auto segment = [&](const int qblk, const int kb0, const int kb1, const int chunk, const int nchunks) {
+#ifdef BT_TIMELINE
+    unsigned long long tl[8] = {};
+#endif
+    BT_TL(0);
     const int wg_q0 = qblk * pos_per_wg;
     const int q0 = wg_q0 + (wave / G) * kQ8;
     const int last = kb1 - 1;
@@ -281,6 +311,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       if constexpr (LO) eq = q_row_f16_lo(reinterpret_cast<const float*>(p.q), off, 32, qop, qlo, reduce);
       else eq = q_row_f16(p.q, p.q_f32 != 0, off, 32, qop, reduce);
       c_col = __builtin_ldexpf(p.scale_log2, eq);
+      BT_TL(1);
     }
     if constexpr (DIRECT) {
       // Block maxima (bf16 bits of |x|, which order like |x|): V over waves
@@ -482,6 +513,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     u32x4 f0[4];
     wait_all();
     __syncthreads();
+    BT_TL(2);
     {
       floatx4 sacc[4];
       k_first(Buf8<0>{}, f0);
@@ -496,6 +528,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       eb_c = eb_n;
       end_block(Buf8<1>{}, f0);  // K_{kb0+1} arrived with the prologue's copies
     }
+    BT_TL(3);
     // Block kb: A: S_kb = K_kb . Q^T; B: O += V_{kb-1} . P_{kb-1} beside the
     // softmax of S_kb.
     auto step = [&](auto b, int kb) {
@@ -535,9 +568,11 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       step(Buf8<0>{}, kb + 1);
     }
     if (kb < kb1) step(Buf8<1>{}, kb);
+    BT_TL(4);
     wait_all();
     barrier();
     if ((last - kb0) & 1) pv(Buf8<1>{}, pk); else pv(Buf8<0>{}, pk);
+    BT_TL(5);
 
     // ---- epilogue: row sums over the four lane groups, normalise, store -------
     l_run = xor_sum<16>(l_run);
@@ -583,6 +618,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       unsigned char* prows = reinterpret_cast<unsigned char*>(p.part + (slot * kRows8 + wave * kQ8) * D);
       store_f32([&](int r) -> unsigned char* { return prows + r * (D * 4); });
       if (g4 == 0) p.lse[slot * kRows8 + wave * kQ8 + i16] = l_run > 0.f ? fast_log2(l_run) + m_ref : -INFINITY;
+      BT_TL_END();
       return;
     }
     auto out_row = [&](int r) -> unsigned char* {
@@ -602,6 +638,7 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
     } else {
       store_f32(out_row);
     }
+    BT_TL_END();
   };
   auto n_blocks = [&](int qb) { return (P0 + min(S, (qb + 1) * pos_per_wg) + kKB8 - 1) / kKB8; };
   if constexpr (PAIRED) {
@@ -844,3 +881,16 @@ hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t str
 }
 
 }  // namespace bt
+
+#ifdef BT_TIMELINE
+// Timeline build only (libbt_timeline.so, built beside the product library,
+// never loaded by it): copy out or clear the recorded timestamps.
+extern "C" int bt_timeline_read(unsigned long long* host, int n) {
+  if (n < 0 || n > bt::kTimelineSlots) return -22;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(bt::bt_tl_buf), (size_t)n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+extern "C" int bt_timeline_clear() {
+  static unsigned long long zero[bt::kTimelineSlots];
+  return hipMemcpyToSymbol(HIP_SYMBOL(bt::bt_tl_buf), zero, sizeof(zero), 0, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1;
+}
+#endif
