@@ -767,15 +767,17 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
   // (384 slots) took 45.5 us against 34.4 us for 4-block chunks (256 slots)
   // and 44.2 us unsplit; at S = 2048, 16-block chunks (256 slots) took 54.7 us
   // against 62.9 us for 11-block chunks (384 slots) and 71.5 us unsplit.
-  // Chunks are at least two key blocks long (one-block chunks: S = 128 24.5 vs
-  // 22.3 us, S = 256 23.5 vs 25.2 us, S = 512 unchanged) and a query block has
-  // at most kMaxChunks.  A grid with a work-group per CU or more is not split
+  // A chunk may be a single key block: with the staged epilogue (partials
+  // stored as whole row slices) one-block chunks beat two-block ones at
+  // config 4, S = 128 / 192 / 256 / 384 / 512: 13.8 / 16.6 / 17.9 / 19.3 /
+  // 20.0 -> 13.2 / 14.1 / 14.8 / 16.1 / 18.6 us per call (before it, S = 128
+  // measured 24.5 against 22.3 us).  A query block has at most kMaxChunks.  A grid with a work-group per CU or more is not split
   // (the heavy-first launch order balances it as far as it can).
   int uniform = 0;          // its chunk length (0: no uniform split)
   int longest = nkb_max;    // key blocks of the busiest work-group
   if ((int64_t)nqb * kv_heads < num_cus) {
     const int max_chunks = min(num_cus / (nqb * kv_heads), kMaxChunks);
-    const int lo = max(2, (nkb_max + max_chunks - 1) / max_chunks);
+    const int lo = (nkb_max + max_chunks - 1) / max_chunks;
     if (lo < nkb_max) {
       uniform = lo;
       longest = lo;

@@ -259,7 +259,7 @@ def test_gemv_refuses_bad_arguments_and_sizes_its_workspace():
         (128, 8192, 16, 15),
         (512, 16384, 16, 4),
         (256, 4096, 8, 14),
-        (512, 0, 8, 4),
+        (512, 0, 8, 8),  # one-block chunks
         (2048, 0, 8, 2),
         (1024, 0, 8, 4),
         # the paired split (pairs of query blocks r and nqb-1-r, each cut into
