@@ -783,6 +783,16 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
       longest = lo;
     }
   }
+  // Two-block chunks convert their tiles in the work-group (no pre-pass, see
+  // DIRECT); they are taken over longer chunks while their grid stays within
+  // 1.6 rounds of the CUs: config 4, S = 768 / 896 24.5 / 27.2 -> 22.6 / 25.9
+  // us per call (288 / 392 slots); at S = 1024 (two full rounds, 512 slots)
+  // 27.8 -> 38.6 us.
+  if (nkb_max > 2 && (uniform == 0 || uniform > 2) && (nkb_max + 1) / 2 <= kMaxChunks &&
+      5 * (int64_t)nqb * kv_heads * ((nkb_max + 1) / 2) <= 8 * (int64_t)num_cus) {
+    uniform = 2;
+    longest = 2;
+  }
   // The paired split balances the causal triangle: a pair of query blocks
   // has about the same key blocks for every pair.  It pays a second q load
   // and epilogue in work-groups that cover two segments, more partials, and a
