@@ -90,6 +90,11 @@ struct PrefillParams {
   // its log2-domain LSE per (query, head) row and chunk, merged by
   // prefill_combine_kernel.  kb_chunk = 0: one work-group per query block.
   int32_t kb_chunk;
+  // split_compact = 1: the uniform split's grid x lists only the (chunk, kv
+  // head subset, query block) items that have keys, each chunk's query blocks
+  // padded to a multiple of 8 (grid y = z = 1); 0: grid (query blocks, kv
+  // heads x subsets, max_chunks), the items past a query block's keys exiting.
+  int32_t split_compact;
   // Paired split (pair_parts > 0, kb_chunk = 0): query blocks nqb-1-r and r
   // form pair r; the pair's key blocks (those of nqb-1-r, then those of r) are
   // cut into pair_parts equal ranges, one per work-group (grid x = pairs x
@@ -105,6 +110,7 @@ struct PrefillParams {
 // per query block would leave CUs idle (short prompts, long cached prefixes).
 struct PrefillSplitPlan {
   int32_t kb_chunk = 0;    // 0: no uniform split
+  int32_t compact = 0;     // uniform split on the compact grid (see PrefillParams)
   int32_t pair_parts = 0;  // 0: no paired split
   int32_t max_chunks = 1;
   int32_t query_blocks = 0;

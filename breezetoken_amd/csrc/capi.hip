@@ -528,6 +528,7 @@ static int prefill_run(const void* q, int32_t q_dtype, const void* k, const void
     const bt::PrefillSplitPlan plan = prefill_plan(seqlen, q_offset, heads, kv_heads, head_dim, &part_offset);
     if (plan.active() && (!plan.uses_partials() || (partials && partials_bytes >= (int64_t)plan.part_bytes))) {
       p.kb_chunk = plan.kb_chunk;
+      p.split_compact = plan.compact;
       p.pair_parts = plan.pair_parts;
       p.max_chunks = plan.max_chunks;
       if (plan.uses_partials()) {

@@ -106,6 +106,28 @@ __host__ __device__ inline int pair_chunks(int qb, int nqb, int parts, NB n_bloc
   return qb == qhi ? (nhi + size - 1) / size : (nhi + nlo - 1) / size - nhi / size + 1;
 }
 
+// Query blocks with more than c chunks of kb key blocks under the uniform
+// split: the heaviest n of them (query blocks nqb - n .. nqb - 1), since a
+// query block's key blocks grow with its index (block qb ends at position
+// min(S, (qb + 1) * pos) behind P0 cached keys).
+__host__ __device__ inline int split_blocks_past(int c, int kb, int S, int P0, int pos, int nqb) {
+  const int R = c * kb * kKB8 - P0;  // positions a query block must pass
+  if (R < 0) return nqb;
+  if (S <= R) return 0;
+  return nqb - R / pos;
+}
+// Work-groups of the uniform split's compact grid for one (kv head, head
+// subset): per chunk c, one per query block with keys there, rounded up to a
+// multiple of 8 so that every chunk of query block qb runs on the XCD of
+// work-group id (nqb - 1 - qb) mod 8, whose L2 then holds all of its partials
+// for the combine (which places its merge the same way).
+__host__ __device__ inline int split_pad8(int n) { return (n + 7) & ~7; }
+__host__ __device__ inline int split_items(int kb, int S, int P0, int pos, int nqb, int max_chunks) {
+  int n = 0;
+  for (int c = 0; c < max_chunks; ++c) n += split_pad8(split_blocks_past(c, kb, S, P0, pos, nqb));
+  return n;
+}
+
 }  // namespace
 
 // Timeline build only (-DBT_TIMELINE, libbt_timeline.so; never the product
@@ -167,16 +189,39 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int ysub = blockIdx.y;              // (kv head, head subset)
-  const int kvh = ysub / p.head_subs;
   const int G = p.sub_group;                // 1, 2, 4 or 8 (checked by the launcher)
-  const int head_base = kvh * p.group + (ysub % p.head_subs) * G;
   const int pos_per_wg = kQ8 * (kWaves8 / G);
   const int S = p.seqlen;
   const int P0 = p.q_offset;
   const int nkeys = P0 + S;
   const int nqb = (S + pos_per_wg - 1) / pos_per_wg;
   const int nblk = (nkeys + kKB8 - 1) / kKB8;
+  // (kv head, head subset): grid y, or under the uniform split part of the
+  // compact grid's x, which lists the (chunk, subset, query block) items that
+  // have keys, chunk slowest and the heaviest query block first (the order of
+  // a full chunks x subsets x query blocks grid without its empty slots).
+  int ysub = blockIdx.y, split_qb = 0, split_chunk = 0;
+  if (!PAIRED && p.kb_chunk > 0 && p.split_compact) {
+    const int ys = p.kv_heads * p.head_subs;
+    int L = (int)blockIdx.x;
+    bool found = false;
+    for (int c = 0; c < p.max_chunks && !found; ++c) {
+      const int n = split_blocks_past(c, p.kb_chunk, S, P0, pos_per_wg, nqb);
+      const int np = split_pad8(n);
+      if (L < np * ys) {
+        if (L % np >= n) return;  // a padding slot (whole work-group)
+        ysub = L / np;
+        split_qb = nqb - 1 - L % np;
+        split_chunk = c;
+        found = true;
+      } else {
+        L -= np * ys;
+      }
+    }
+    if (!found) return;  // past the launcher's item count: no work-group is
+  }
+  const int kvh = ysub / p.head_subs;
+  const int head_base = kvh * p.group + (ysub % p.head_subs) * G;
   // One segment: key blocks [kb0, kb1) of query block qblk, chunk `chunk` of
   // its nchunks (nchunks > 1: the segment writes a partial for the combine).
   auto segment = [&](const int qblk, const int kb0, const int kb1, const int chunk, const int nchunks) {
@@ -660,16 +705,20 @@ __global__ __launch_bounds__(kWaves8 * 64, 1) void gqa_prefill8_kernel(PrefillPa
       segment(qlo, max(0, r0 - nhi), r1 - nhi, k - kfirst, (nhi + nlo - 1) / size - kfirst + 1);
     }
   } else {
-    const int qblk = nqb - 1 - (int)blockIdx.x;  // heavy blocks first
-    const int nkb = n_blocks(qblk);
-    // Key blocks of this work-group: all of them, or chunk blockIdx.z.
+    // Key blocks of this work-group: all of its query block's (heavy blocks
+    // first), or one chunk of them.
     if (p.kb_chunk > 0) {
-      const int chunk = blockIdx.z;
-      const int kb0 = chunk * p.kb_chunk;
+      if (!p.split_compact) {  // grid (query block, subset, chunk)
+        split_qb = nqb - 1 - (int)blockIdx.x;
+        split_chunk = blockIdx.z;
+      }
+      const int nkb = n_blocks(split_qb);
+      const int kb0 = split_chunk * p.kb_chunk;
       if (kb0 >= nkb) return;  // this query block has fewer chunks (whole work-group)
-      segment(qblk, kb0, min(nkb, kb0 + p.kb_chunk), chunk, (nkb + p.kb_chunk - 1) / p.kb_chunk);
+      segment(split_qb, kb0, min(nkb, kb0 + p.kb_chunk), split_chunk, (nkb + p.kb_chunk - 1) / p.kb_chunk);
     } else {
-      segment(qblk, 0, nkb, 0, 1);
+      const int qblk = nqb - 1 - (int)blockIdx.x;
+      segment(qblk, 0, n_blocks(qblk), 0, 1);
     }
   }
 }
@@ -775,6 +824,7 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
   // (the heavy-first launch order balances it as far as it can).
   int uniform = 0;          // its chunk length (0: no uniform split)
   int longest = nkb_max;    // key blocks of the busiest work-group
+  bool compact = false;
   if ((int64_t)nqb * kv_heads < num_cus) {
     const int max_chunks = min(num_cus / (nqb * kv_heads), kMaxChunks);
     const int lo = (nkb_max + max_chunks - 1) / max_chunks;
@@ -792,6 +842,26 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
       5 * (int64_t)nqb * kv_heads * ((nkb_max + 1) / 2) <= 8 * (int64_t)num_cus) {
     uniform = 2;
     longest = 2;
+  }
+  // The compact grid drops the slots of chunks past a query block's keys, so
+  // shorter chunks fit one round; it is taken where that shortens a work-group
+  // by over 15%, counting ~4 key blocks of fixed cost per segment: config 4,
+  // S = 1280 / 1536 / 2048 32.1 / 39.4 / 46.9 -> 30.6 / 34.2 / 43.3 us per
+  // call (chunks of 7 / 12 / 16 -> 4 / 6 / 12 blocks).  Where it would not,
+  // it measured slower (S = 128 / 512 / 1024 +0.5 / +0.6 / +0.6 us).
+  if (uniform > 0 && 2 * (int64_t)nqb * kv_heads <= num_cus) {
+    for (int kb = 1; kb < uniform; ++kb) {
+      const int mc = (nkb_max + kb - 1) / kb;
+      if (mc <= kMaxChunks &&
+          (int64_t)kv_heads * split_items(kb, seqlen, q_offset, pos_per_wg, nqb, mc) <= num_cus) {
+        if (100 * (kb + 4) < 85 * (uniform + 4)) {
+          uniform = kb;
+          longest = kb;
+          compact = true;
+        }
+        break;
+      }
+    }
   }
   // The paired split balances the causal triangle: a pair of query blocks
   // has about the same key blocks for every pair.  It pays a second q load
@@ -816,6 +886,7 @@ PrefillSplitPlan prefill8_split_plan(int seqlen, int q_offset, int group, int kv
     plan.max_chunks = mc;
   } else if (uniform > 0) {
     plan.kb_chunk = uniform;
+    plan.compact = compact ? 1 : 0;
     plan.max_chunks = (nkb_max + uniform - 1) / uniform;
   } else {
     return plan;
@@ -844,7 +915,9 @@ hipError_t launch_prefill8(const PrefillParams& p, int head_dim, hipStream_t str
   if (split && (p.max_chunks < 1 || p.max_chunks > kMaxChunks || !p.part || !p.lse)) return hipErrorInvalidValue;
   const int ys = p.kv_heads * p.head_subs;  // grid y: (kv head, head subset)
   const dim3 grid = paired ? dim3(((nqb + 1) / 2) * p.pair_parts, ys, 1)
-                           : dim3(nqb, ys, p.kb_chunk > 0 ? p.max_chunks : 1);
+                   : p.kb_chunk > 0 && p.split_compact
+                       ? dim3(ys * split_items(p.kb_chunk, p.seqlen, p.q_offset, pos_per_wg, nqb, p.max_chunks), 1, 1)
+                       : dim3(nqb, ys, p.kb_chunk > 0 ? p.max_chunks : 1);
   // The combine's work-groups run the query blocks heaviest first; under the
   // uniform split only the heaviest ones have more than one chunk (a query
   // block's key blocks grow with its index), so its grid stops there -- at a

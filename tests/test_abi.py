@@ -260,7 +260,7 @@ def test_gemv_refuses_bad_arguments_and_sizes_its_workspace():
         (512, 16384, 16, 4),
         (256, 4096, 8, 14),
         (512, 0, 8, 8),  # one-block chunks
-        (2048, 0, 8, 2),
+        (2048, 0, 8, 3),  # 12-block chunks: 240 work-groups in the compact grid
         (1024, 0, 8, 4),
         # the paired split (pairs of query blocks r and nqb-1-r, each cut into
         # 2 equal ranges): at most 2 ranges reach a query block
